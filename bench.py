@@ -1,0 +1,365 @@
+#!/usr/bin/env python3
+"""Benchmark of the static-lm attention hot path on one MI355X.
+
+Headline (`value`): decode attention HBM throughput at 32k context on the
+Llama-3-8B head shape (32 heads over 8 KV heads, head_dim 128, f32 KV).  One
+step is one decode token through 8 layers whose KV caches (256 MiB each,
+2 GiB together) are rotated so the 256 MB Infinity Cache cannot serve them:
+per layer the KV append at position 32767, then attention over rows
+0..32767.  Algorithmic bytes per layer-step:
+    B(p) = 4 * (2*(p+1)*kv_dim + 2*dim + 4*kv_dim)
+(K and V rows 0..p read once, shared by the 4 query heads of each KV head;
+q in, out; k, v in; K, V row written).
+
+Also reported: causal prefill of 4096 tokens (1 layer, same shape) in
+TFLOP/s with F = 4*hd*H*sum_{p=1..4096} p, and 64 decode steps at 131072+
+context (1 GiB KV, one layer).
+
+Inputs are synthetic N(0,1)*0.5 f32 drawn on the GPU and resident in HBM
+before timing.  The CPU baseline is the CPU oracle (the reference's
+single-threaded attention arithmetic restated in C) timed on a bounded
+sample on one host core.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+METRIC = "decode attn HBM GB/s @32k ctx; prefill attn TFLOP/s @4k; % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+DIM, HEADS, KV_HEADS = 4096, 32, 8
+HD = DIM // HEADS
+KV_DIM = HD * KV_HEADS
+THETA = 500000.0
+
+
+def load_product():
+    name = "static_lm_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, REPO / "static-lm_amd" / "__init__.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def decode_bytes(pos: int) -> int:
+    return 4 * (2 * (pos + 1) * KV_DIM + 2 * DIM + 4 * KV_DIM)
+
+
+def prefill_flops(start: int, n: int) -> int:
+    s = sum(range(start + 1, start + n + 1))
+    return 4 * HD * HEADS * s
+
+
+def host_cpu() -> str:
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def fill_cache(torch, ctx, layers: int, msl: int, rows: int, seed: int) -> None:
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    blk = 8192
+    buf = torch.empty(blk * KV_DIM, device="cuda", dtype=torch.float32)
+    for layer in range(layers):
+        for which in (0, 1):
+            for p0 in range(0, rows, blk):
+                n = min(blk, rows - p0)
+                torch.randn(blk * KV_DIM, generator=g, device="cuda", out=buf)
+                buf.mul_(0.5)
+                ctx.kv_write_dev(layer, which, p0, n, buf.data_ptr())
+    ctx.sync()
+
+
+def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
+    layers, ctx_len = 8, 32768
+    pos = ctx_len - 1
+    ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, ctx_len, layers, THETA)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    fill_cache(torch, ctx, layers, ctx_len, ctx_len, 1234)
+    q = torch.randn(layers, DIM, device="cuda") * 0.5
+    k = torch.randn(layers, KV_DIM, device="cuda") * 0.5
+    v = torch.randn(layers, KV_DIM, device="cuda") * 0.5
+    out = torch.empty(layers, DIM, device="cuda")
+
+    def step():
+        for l in range(layers):
+            ctx.decode_dev(l, pos, q[l].data_ptr(), k[l].data_ptr(), v[l].data_ptr(),
+                           out[l].data_ptr())
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1)
+
+    # second pass with per-launch events, for the dominant kernel's duration
+    ctx.profile(True)
+    for _ in range(steps):
+        step()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    n_split, split_ms = prof["decode_split"]
+    avg_split_s = split_ms / max(n_split, 1) / 1e3
+    kv_bytes = 2 * (pos + 1) * KV_DIM * 4
+    achieved = kv_bytes / avg_split_s / 1e9
+    ns, chunk = ctx.decode_splits(pos + 1)
+    finite = bool(torch.isfinite(out).all().item())
+    ctx.close()
+    step_bytes = layers * decode_bytes(pos)
+    return {
+        "ms": ms, "wall_s": wall, "steps": steps, "layers": layers, "pos": pos,
+        "step_bytes": step_bytes, "gbs": step_bytes * steps / (ms / 1e3) / 1e9,
+        "profile": prof, "split_kernel_avg_us": avg_split_s * 1e6,
+        "split_kernel_bytes": kv_bytes, "split_kernel_gbs": achieved,
+        "splits": ns, "chunk": chunk, "finite": finite,
+    }
+
+
+def bench_prefill_4k(torch, P, reps: int) -> dict:
+    n, msl = 4096, 8192
+    ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, msl, 1, THETA)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    q = torch.randn(n, DIM, device="cuda") * 0.5
+    k = torch.randn(n, KV_DIM, device="cuda") * 0.5
+    v = torch.randn(n, KV_DIM, device="cuda") * 0.5
+    out = torch.empty(n, DIM, device="cuda")
+
+    def run():
+        ctx.prefill_dev(0, 0, n, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
+
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    ctx.profile(True)
+    for _ in range(reps):
+        run()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    cnt, kms = prof["prefill"]
+    flops = prefill_flops(0, n)
+    kern_s = kms / max(cnt, 1) / 1e3
+    ctx.close()
+    return {"ms": ms, "reps": reps, "flops": flops, "tflops": flops / (ms / 1e3) / 1e12,
+            "kernel_avg_ms": kern_s * 1e3, "kernel_tflops": flops / kern_s / 1e12,
+            "profile": prof}
+
+
+def bench_decode_131k(torch, P) -> dict:
+    pre, steps = 131072, 64
+    msl = pre + steps
+    ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, msl, 1, THETA)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    fill_cache(torch, ctx, 1, msl, pre, 99)
+    q = torch.randn(steps, DIM, device="cuda") * 0.5
+    k = torch.randn(steps, KV_DIM, device="cuda") * 0.5
+    v = torch.randn(steps, KV_DIM, device="cuda") * 0.5
+    out = torch.empty(steps, DIM, device="cuda")
+
+    def run():
+        for s in range(steps):
+            ctx.decode_dev(0, pre + s, q[s].data_ptr(), k[s].data_ptr(), v[s].data_ptr(),
+                           out[s].data_ptr())
+
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    total = sum(decode_bytes(pre + s) for s in range(steps))
+    ctx.close()
+    return {"ms_total": ms, "steps": steps, "ms_per_step": ms / steps, "bytes": total,
+            "gbs": total / (ms / 1e3) / 1e9}
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The oracle's decode (rope + append + JIT-softmax attention) at position
+    32767 of one layer of the same shape, on one host core, repeated until
+    the time budget is spent; plus a sample of prefill rows."""
+    import numpy as np
+
+    sys.path.insert(0, str(REPO))
+    from oracle import py_oracle as orc
+
+    ctx_len = 32768
+    pos = ctx_len - 1
+    cfg = orc.Cfg(DIM, HEADS, KV_HEADS, ctx_len, 1, THETA)
+    om = orc.OracleModel(cfg)
+    rng = np.random.default_rng(5)
+    om.k_cache(0)[:] = rng.standard_normal((ctx_len, KV_DIM), dtype=np.float32) * 0.5
+    om.v_cache(0)[:] = rng.standard_normal((ctx_len, KV_DIM), dtype=np.float32) * 0.5
+    q = rng.standard_normal(DIM, dtype=np.float32) * 0.5
+    k = rng.standard_normal(KV_DIM, dtype=np.float32) * 0.5
+    v = rng.standard_normal(KV_DIM, dtype=np.float32) * 0.5
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        om.decode(0, pos, q, k, v)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s * 0.75:
+            break
+    dec_gbs = decode_bytes(pos) * calls / el / 1e9
+    # prefill sample: the last rows of a 4096-token prefill, each attending
+    # to 4090+ cached rows (the per-row loop of the reference)
+    pcfg = orc.Cfg(DIM, HEADS, KV_HEADS, 4096, 1, THETA)
+    pm = orc.OracleModel(pcfg)
+    pm.k_cache(0)[:] = rng.standard_normal((4096, KV_DIM), dtype=np.float32) * 0.5
+    pm.v_cache(0)[:] = rng.standard_normal((4096, KV_DIM), dtype=np.float32) * 0.5
+    rows = 0
+    flops = 0
+    t1 = time.perf_counter()
+    while True:
+        p = 4095 - rows
+        pm.attend(0, q, p)
+        flops += 4 * HD * HEADS * (p + 1)
+        rows += 1
+        el2 = time.perf_counter() - t1
+        if el2 >= budget_s * 0.25:
+            break
+    return {
+        "value": dec_gbs, "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"{calls} oracle decode calls (rope+append+attention) at pos {pos}, one layer, "
+                  f"{el:.1f} s on {host_cpu()} (nproc {os.cpu_count()})",
+        "prefill_tflops": flops / el2 / 1e12,
+        "prefill_sample": f"last {rows} rows of a 4096-token prefill, {el2:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0,
+                    help="time budget of the CPU baseline sample (0 skips it)")
+    ap.add_argument("--skip-extra", action="store_true",
+                    help="only the headline decode @32k measurement")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
+              "(sharding is design only); run it with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    P = load_product()
+    P.load_library()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    torch.manual_seed(0)
+    log(f"device {torch.cuda.get_device_name(0)}")
+
+    log("decode @32k")
+    d = bench_decode_32k(torch, P, args.steps, args.warmup)
+    log(f"decode @32k: {d['gbs']:.1f} GB/s, split kernel {d['split_kernel_avg_us']:.1f} us "
+        f"({d['split_kernel_gbs']:.1f} GB/s)")
+    extra = {}
+    if not args.skip_extra:
+        log("prefill 4096")
+        pf = bench_prefill_4k(torch, P, reps=max(3, args.steps // 10))
+        log(f"prefill 4096: {pf['ms']:.3f} ms, {pf['tflops']:.2f} TFLOP/s")
+        log("decode @131k")
+        dl = bench_decode_131k(torch, P)
+        log(f"decode @131k: {dl['ms_per_step']*1e3:.1f} us/step, {dl['gbs']:.1f} GB/s")
+        extra = {
+            "prefill_4k": {
+                "tflops": pf["tflops"], "ms": pf["ms"], "flops": pf["flops"],
+                "frac_fp32_mfma": pf["tflops"] / FP32_MFMA_PEAK_TFLOPS,
+                "kernel_avg_ms": pf["kernel_avg_ms"], "kernel_tflops": pf["kernel_tflops"],
+                "workload": "causal prefill 4096 tokens, 1 layer, start 0",
+            },
+            "decode_131k": {
+                "gbs": dl["gbs"], "us_per_step": dl["ms_per_step"] * 1e3,
+                "frac_hbm": dl["gbs"] / HBM_PEAK_GBS,
+                "workload": "64 decode steps at positions 131072..131135, 1 layer, 1 GiB KV",
+            },
+        }
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("cpu baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    ms_per_step = d["ms"] / d["steps"]
+    res = {
+        "metric": METRIC,
+        "value": round(d["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode attention @32k ctx, Llama-3-8B head shape (32 heads / 8 KV heads, "
+                        "head_dim 128), 8 layers of f32 KV rotated per step",
+            "dim": DIM, "num_heads": HEADS, "num_kv_heads": KV_HEADS, "head_dim": HD,
+            "ctx": d["pos"] + 1, "layers": d["layers"], "rope_theta": THETA,
+            "bytes_per_step": d["step_bytes"], "splits": d["splits"], "chunk": d["chunk"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attn_rows_kernel<128,4> (split-K decode)",
+            "achieved": round(d["split_kernel_gbs"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(d["split_kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(d["split_kernel_avg_us"], 3),
+            "algorithmic_bytes_per_launch": d["split_kernel_bytes"],
+        },
+        "cpu_baseline": cpu,
+        "frac_hbm_step": round(d["gbs"] / HBM_PEAK_GBS, 4),
+        **extra,
+    }
+    print(json.dumps(res))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

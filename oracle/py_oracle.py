@@ -1,0 +1,240 @@
+"""ctypes binding of the C oracle (liboracle.so) -- test infrastructure only.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use
+this module, as the checker.  Functions restate static-lm's CPU arithmetic;
+see slm_oracle.h for the reference lines each one follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "liboracle.so"
+
+
+class OrcConfig(ctypes.Structure):
+    _fields_ = [
+        ("dim", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("max_seq_len", ctypes.c_int32),
+        ("num_layers", ctypes.c_int32),
+        ("rope_theta", ctypes.c_float),
+    ]
+
+
+_F = ctypes.POINTER(ctypes.c_float)
+_D = ctypes.POINTER(ctypes.c_double)
+_C = ctypes.POINTER(OrcConfig)
+_SZ = ctypes.c_size_t
+_I = ctypes.c_int
+
+_SIGS = {
+    "orc_validate": (ctypes.c_int, [_C]),
+    "orc_rope_tables": (None, [_I, _I, ctypes.c_float, _F, _F]),
+    "orc_apply_rope_cached": (None, [_F, _SZ, _F, _F, _I]),
+    "orc_apply_rope_in_place": (None, [_F, _SZ, _I, _I, ctypes.c_float]),
+    "orc_jit_exp": (ctypes.c_float, [ctypes.c_float]),
+    "orc_jit_exp_array": (None, [_F, _F, _SZ]),
+    "orc_softmax_jit": (None, [_F, _SZ]),
+    "orc_softmax_scalar": (None, [_F, _SZ]),
+    "orc_attention_jit": (None, [_F, _F, _F, _F, _F, _C, _I]),
+    "orc_attention_scalar": (None, [_F, _F, _F, _F, _F, _C, _I]),
+    "orc_kv_offset": (_SZ, [_C, _I, _I, _I]),
+    "orc_decode": (None, [_C, _F, _F, _F, _I, _I, _F, _F, _F, _F, _F, _F]),
+    "orc_prefill": (None, [_C, _F, _F, _F, _I, _I, _I, _F, _F, _F, _F, _F, _F]),
+    "orc_attention_f64": (None, [_F, _F, _F, _D, _C, _I]),
+}
+
+_lib = None
+
+
+def build() -> Path:
+    """Compiles liboracle.so with oracle/Makefile (gcc, no fast-math)."""
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+@dataclass(frozen=True)
+class Cfg:
+    dim: int
+    num_heads: int
+    num_kv_heads: int
+    max_seq_len: int
+    num_layers: int = 1
+    rope_theta: float = 10000.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.dim // self.num_heads
+
+    @property
+    def kv_dim(self) -> int:
+        return self.head_dim * self.num_kv_heads
+
+    @property
+    def kv_mul(self) -> int:
+        return self.num_heads // self.num_kv_heads
+
+    def c(self) -> OrcConfig:
+        return OrcConfig(self.dim, self.num_heads, self.num_kv_heads, self.max_seq_len,
+                         self.num_layers, self.rope_theta)
+
+
+def validate(cfg: Cfg) -> int:
+    c = cfg.c()
+    return lib().orc_validate(ctypes.byref(c))
+
+
+def rope_tables(head_dim: int, max_seq_len: int, theta: float = 10000.0):
+    half = head_dim // 2
+    c = np.empty((max_seq_len, half), np.float32)
+    s = np.empty((max_seq_len, half), np.float32)
+    lib().orc_rope_tables(head_dim, max_seq_len, theta, _p(c), _p(s))
+    return c, s
+
+
+def apply_rope_cached(vec, cos_row, sin_row, head_dim: int) -> np.ndarray:
+    v = _f32(vec).copy()
+    c, s = _f32(cos_row), _f32(sin_row)
+    lib().orc_apply_rope_cached(_p(v), v.size, _p(c), _p(s), head_dim)
+    return v
+
+
+def apply_rope_in_place(vec, pos: int, head_dim: int, theta: float = 10000.0) -> np.ndarray:
+    v = _f32(vec).copy()
+    lib().orc_apply_rope_in_place(_p(v), v.size, pos, head_dim, theta)
+    return v
+
+
+def jit_exp(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_jit_exp_array(_p(x), _p(out), x.size)
+    return out
+
+
+def softmax_jit(x) -> np.ndarray:
+    v = _f32(x).copy()
+    lib().orc_softmax_jit(_p(v), v.size)
+    return v
+
+
+def softmax_scalar(x) -> np.ndarray:
+    v = _f32(x).copy()
+    lib().orc_softmax_scalar(_p(v), v.size)
+    return v
+
+
+def attention(q_rot, k_cache, v_cache, cfg: Cfg, pos: int, jit: bool = True) -> np.ndarray:
+    """causal_multi_head_attention{_jit} over one layer's [msl][kv_dim] slices."""
+    q = _f32(q_rot)
+    kc, vc = _f32(k_cache), _f32(v_cache)
+    att = np.empty(cfg.num_heads * cfg.max_seq_len, np.float32)
+    out = np.empty(cfg.dim, np.float32)
+    c = cfg.c()
+    fn = lib().orc_attention_jit if jit else lib().orc_attention_scalar
+    fn(_p(q), _p(kc), _p(vc), _p(att), _p(out), ctypes.byref(c), pos)
+    return out
+
+
+def attention_f64(q_rot, k_cache, v_cache, cfg: Cfg, pos: int) -> np.ndarray:
+    q = _f32(q_rot)
+    kc, vc = _f32(k_cache), _f32(v_cache)
+    out = np.empty(cfg.dim, np.float64)
+    c = cfg.c()
+    lib().orc_attention_f64(_p(q), _p(kc), _p(vc), out.ctypes.data_as(_D), ctypes.byref(c), pos)
+    return out
+
+
+def kv_offset(cfg: Cfg, layer: int, which: int, pos: int) -> int:
+    c = cfg.c()
+    return int(lib().orc_kv_offset(ctypes.byref(c), layer, which, pos))
+
+
+class OracleModel:
+    """The reference's KV arena [L][K|V][msl][kv_dim] plus RoPE tables, driven
+    like TransformerModel drives its layers (decode and prefill blocks)."""
+
+    def __init__(self, cfg: Cfg):
+        self.cfg = cfg
+        self.kv = np.zeros(2 * cfg.num_layers * cfg.max_seq_len * cfg.kv_dim, np.float32)
+        self.cos, self.sin = rope_tables(cfg.head_dim, cfg.max_seq_len, cfg.rope_theta)
+        self._att = np.empty(cfg.num_heads * cfg.max_seq_len, np.float32)
+
+    def k_cache(self, layer: int) -> np.ndarray:
+        S = self.cfg.max_seq_len * self.cfg.kv_dim
+        return self.kv[(2 * layer) * S:(2 * layer + 1) * S].reshape(self.cfg.max_seq_len, -1)
+
+    def v_cache(self, layer: int) -> np.ndarray:
+        S = self.cfg.max_seq_len * self.cfg.kv_dim
+        return self.kv[(2 * layer + 1) * S:(2 * layer + 2) * S].reshape(self.cfg.max_seq_len, -1)
+
+    def decode(self, layer: int, pos: int, q, k, v) -> np.ndarray:
+        cfg = self.cfg
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        q_rot = np.empty(cfg.dim, np.float32)
+        out = np.empty(cfg.dim, np.float32)
+        c = cfg.c()
+        lib().orc_decode(ctypes.byref(c), _p(self.kv), _p(self.cos), _p(self.sin), layer, pos,
+                         _p(q), _p(k), _p(v), _p(q_rot), _p(self._att), _p(out))
+        return out
+
+    def prefill(self, layer: int, start: int, q, k, v) -> np.ndarray:
+        cfg = self.cfg
+        q = _f32(q).reshape(-1, cfg.dim)
+        n = q.shape[0]
+        k, v = _f32(k), _f32(v)
+        q_rot = np.empty_like(q)
+        out = np.empty_like(q)
+        c = cfg.c()
+        lib().orc_prefill(ctypes.byref(c), _p(self.kv), _p(self.cos), _p(self.sin), layer, start,
+                          n, _p(q), _p(k), _p(v), _p(q_rot), _p(self._att), _p(out))
+        return out
+
+    def append(self, layer: int, pos0: int, k_rows, v_rows) -> None:
+        """Only the cache side of a decode/prefill block: K rows pos0.. get
+        rope(k), V rows get v (transformer.rs:545-561 then 575-578)."""
+        k_rows = _f32(k_rows).reshape(-1, self.cfg.kv_dim)
+        v_rows = _f32(v_rows).reshape(-1, self.cfg.kv_dim)
+        kc, vc = self.k_cache(layer), self.v_cache(layer)
+        for r in range(k_rows.shape[0]):
+            p = pos0 + r
+            kc[p] = apply_rope_cached(k_rows[r], self.cos[p], self.sin[p], self.cfg.head_dim)
+            vc[p] = v_rows[r]
+
+    def rotated_q(self, q_row, pos: int) -> np.ndarray:
+        return apply_rope_cached(q_row, self.cos[pos], self.sin[pos], self.cfg.head_dim)
+
+    def attend(self, layer: int, q_row, pos: int) -> np.ndarray:
+        """Attention of an un-rotated q row at `pos` over the current cache."""
+        q_rot = self.rotated_q(q_row, pos)
+        return attention(q_rot, self.k_cache(layer), self.v_cache(layer), self.cfg, pos)

@@ -1,0 +1,296 @@
+"""static-lm attention hot path on MI355X (gfx950): Python binding of the
+slm_attn C ABI (include/slm_attn.h).
+
+The compute lives in libslm_attn.so (hand-written HIP kernels); this module
+only marshals buffers through ctypes.  Nothing here computes attention on the
+CPU: if the library is missing, loading it raises.
+
+Names follow the reference (src/model/transformer.rs of static-lm):
+``TransformerConfig`` mirrors transformer.rs:8-33 and ``AttentionContext``
+exposes the attention block of ``TransformerLayer::forward_token_with_kv``
+(transformer.rs:413-443) as ``decode`` and of ``forward_batch_with_kv``
+(transformer.rs:530-593) as ``prefill``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libslm_attn.so"
+HEADER_PATH = PKG_DIR.parent / "include" / "slm_attn.h"
+
+SLM_OK = 0
+ERRORS = {
+    -1: "SLM_ERR_CONFIG",
+    -2: "SLM_ERR_POS",
+    -3: "SLM_ERR_BATCH",
+    -4: "SLM_ERR_LAYER",
+    -5: "SLM_ERR_ALIAS",
+    -6: "SLM_ERR_ARG",
+    -7: "SLM_ERR_HIP",
+    -8: "SLM_ERR_UNSUPPORTED",
+    -9: "SLM_ERR_DEVICE",
+}
+ERR_CONFIG, ERR_POS, ERR_BATCH, ERR_LAYER, ERR_ALIAS, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_DEVICE = (
+    -1, -2, -3, -4, -5, -6, -7, -8, -9)
+
+KERNEL_KINDS = ("append", "decode_split", "decode_combine", "prefill", "rope")
+
+
+class SlmAttnError(RuntimeError):
+    """A nonzero slm_attn return code; the reference would have panicked."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERRORS.get(code, code)}: {message}")
+        self.code = code
+        self.message = message
+
+
+@dataclass(frozen=True)
+class TransformerConfig:
+    """transformer.rs:8-33 (hidden_dim and rms_eps are unused by attention)."""
+
+    dim: int
+    hidden_dim: int
+    num_heads: int
+    num_kv_heads: int
+    max_seq_len: int
+    rms_eps: float = 1e-5
+
+    def head_dim(self) -> int:
+        return self.dim // self.num_heads
+
+    def kv_dim(self) -> int:
+        return (self.dim // self.num_heads) * self.num_kv_heads
+
+    def kv_mul(self) -> int:
+        return self.num_heads // self.num_kv_heads
+
+
+class _Config(ctypes.Structure):
+    _fields_ = [
+        ("dim", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("max_seq_len", ctypes.c_int32),
+        ("num_layers", ctypes.c_int32),
+        ("rope_theta", ctypes.c_float),
+    ]
+
+
+class _KernelStat(ctypes.Structure):
+    _fields_ = [("launches", ctypes.c_int64), ("total_ms", ctypes.c_double)]
+
+
+_F = ctypes.POINTER(ctypes.c_float)
+_P = ctypes.c_void_p
+_I = ctypes.c_int32
+
+# name -> (restype, argtypes); every function the header declares
+SIGNATURES = {
+    "slm_attn_create": (ctypes.c_int, [ctypes.POINTER(_Config), ctypes.POINTER(_P)]),
+    "slm_attn_destroy": (None, [_P]),
+    "slm_attn_last_error": (ctypes.c_char_p, [_P]),
+    "slm_attn_decode": (ctypes.c_int, [_P, _I, _I, _F, _F, _F, _F]),
+    "slm_attn_prefill": (ctypes.c_int, [_P, _I, _I, _I, _F, _F, _F, _F]),
+    "slm_attn_decode_dev": (ctypes.c_int, [_P, _I, _I, _P, _P, _P, _P]),
+    "slm_attn_prefill_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _P, _P]),
+    "slm_rope_apply_dev": (ctypes.c_int, [_P, _P, _I, _I, _I]),
+    "slm_kv_append_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, _P]),
+    "slm_attn_attend_dev": (ctypes.c_int, [_P, _I, _I, _P, _P]),
+    "slm_attn_attend_batch_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, _P]),
+    "slm_attn_set_stream": (ctypes.c_int, [_P, _P]),
+    "slm_attn_get_stream": (_P, [_P]),
+    "slm_attn_sync": (ctypes.c_int, [_P]),
+    "slm_kv_write": (ctypes.c_int, [_P, _I, _I, _I, _I, _F]),
+    "slm_kv_read": (ctypes.c_int, [_P, _I, _I, _I, _I, _F]),
+    "slm_kv_write_dev": (ctypes.c_int, [_P, _I, _I, _I, _I, _P]),
+    "slm_kv_offset": (ctypes.c_size_t, [_P, _I, _I, _I]),
+    "slm_kv_device_ptr": (_P, [_P]),
+    "slm_rope_tables_read": (ctypes.c_int, [_P, _F, _F]),
+    "slm_attn_profile": (ctypes.c_int, [_P, _I]),
+    "slm_attn_profile_read": (ctypes.c_int, [_P, ctypes.POINTER(_KernelStat)]),
+    "slm_attn_decode_splits": (ctypes.c_int, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "slm_attn_version": (ctypes.c_char_p, []),
+}
+
+_lib = None
+
+
+def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
+    """Loads libslm_attn.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(
+            f"{p} is missing: build the HIP library first "
+            "(python static-lm_amd/build.py or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _fptr(a: np.ndarray):
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a, shape=None) -> np.ndarray:
+    arr = np.ascontiguousarray(a, dtype=np.float32)
+    if shape is not None and arr.size != int(np.prod(shape)):
+        raise ValueError(f"expected {shape} floats, got {arr.shape}")
+    return arr
+
+
+class AttentionContext:
+    """One slm_attn context: device KV region [L][K|V][msl][kv_dim] f32 plus
+    RoPE tables, like the KV part of TransformerModel (transformer.rs:714-743)."""
+
+    def __init__(self, dim: int, num_heads: int, num_kv_heads: int, max_seq_len: int,
+                 num_layers: int = 1, rope_theta: float = 10000.0):
+        self.lib = load_library()
+        self.cfg = TransformerConfig(dim, dim, num_heads, num_kv_heads, max_seq_len)
+        self.num_layers = num_layers
+        self.rope_theta = rope_theta
+        c = _Config(dim, num_heads, num_kv_heads, max_seq_len, num_layers, rope_theta)
+        h = _P()
+        rc = self.lib.slm_attn_create(ctypes.byref(c), ctypes.byref(h))
+        if rc != SLM_OK:
+            raise SlmAttnError(rc, self.lib.slm_attn_last_error(None).decode())
+        self._h = h
+
+    # -- lifetime -------------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.slm_attn_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int) -> None:
+        if rc != SLM_OK:
+            raise SlmAttnError(rc, self.lib.slm_attn_last_error(self._h).decode())
+
+    @property
+    def handle(self):
+        return self._h
+
+    # -- host-pointer attention block -------------------------------------------
+    def decode(self, layer: int, pos: int, q, k, v) -> np.ndarray:
+        cfg = self.cfg
+        q = _f32(q, (cfg.dim,))
+        k = _f32(k, (cfg.kv_dim(),))
+        v = _f32(v, (cfg.kv_dim(),))
+        out = np.empty(cfg.dim, np.float32)
+        self._check(self.lib.slm_attn_decode(self._h, layer, pos, _fptr(q), _fptr(k), _fptr(v),
+                                             _fptr(out)))
+        return out
+
+    def prefill(self, layer: int, start: int, q, k, v) -> np.ndarray:
+        cfg = self.cfg
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1, cfg.dim)
+        n = q.shape[0]
+        k = _f32(k, (n, cfg.kv_dim()))
+        v = _f32(v, (n, cfg.kv_dim()))
+        out = np.empty((n, cfg.dim), np.float32)
+        self._check(self.lib.slm_attn_prefill(self._h, layer, start, n, _fptr(q), _fptr(k),
+                                              _fptr(v), _fptr(out)))
+        return out
+
+    # -- device-pointer entry points (addresses as ints) ------------------------
+    def decode_dev(self, layer, pos, q, k, v, out):
+        self._check(self.lib.slm_attn_decode_dev(self._h, layer, pos, q, k, v, out))
+
+    def prefill_dev(self, layer, start, n, q, k, v, out):
+        self._check(self.lib.slm_attn_prefill_dev(self._h, layer, start, n, q, k, v, out))
+
+    def attend_dev(self, layer, pos, q_rot, out):
+        self._check(self.lib.slm_attn_attend_dev(self._h, layer, pos, q_rot, out))
+
+    def attend_batch_dev(self, layer, start, n, q_rot, out):
+        self._check(self.lib.slm_attn_attend_batch_dev(self._h, layer, start, n, q_rot, out))
+
+    def rope_apply_dev(self, x, n, row_len, pos0):
+        self._check(self.lib.slm_rope_apply_dev(self._h, x, n, row_len, pos0))
+
+    def kv_append_dev(self, layer, pos0, n, k, v):
+        self._check(self.lib.slm_kv_append_dev(self._h, layer, pos0, n, k, v))
+
+    # -- streams, cache access, timing ------------------------------------------
+    def set_stream(self, stream: int | None) -> None:
+        self._check(self.lib.slm_attn_set_stream(self._h, stream or None))
+
+    def get_stream(self) -> int:
+        return self.lib.slm_attn_get_stream(self._h) or 0
+
+    def sync(self) -> None:
+        self._check(self.lib.slm_attn_sync(self._h))
+
+    def kv_write(self, layer: int, which: int, pos0: int, rows) -> None:
+        rows = np.ascontiguousarray(rows, dtype=np.float32).reshape(-1, self.cfg.kv_dim())
+        self._check(self.lib.slm_kv_write(self._h, layer, which, pos0, rows.shape[0], _fptr(rows)))
+
+    def kv_write_dev(self, layer: int, which: int, pos0: int, n: int, rows_ptr: int) -> None:
+        self._check(self.lib.slm_kv_write_dev(self._h, layer, which, pos0, n, rows_ptr))
+
+    def kv_read(self, layer: int, which: int, pos0: int, n: int) -> np.ndarray:
+        out = np.empty((n, self.cfg.kv_dim()), np.float32)
+        self._check(self.lib.slm_kv_read(self._h, layer, which, pos0, n, _fptr(out)))
+        return out
+
+    def kv_offset(self, layer: int, which: int, pos: int) -> int:
+        return int(self.lib.slm_kv_offset(self._h, layer, which, pos))
+
+    def kv_device_ptr(self) -> int:
+        return self.lib.slm_kv_device_ptr(self._h) or 0
+
+    def rope_tables(self) -> tuple[np.ndarray, np.ndarray]:
+        half = self.cfg.head_dim() // 2
+        c = np.empty((self.cfg.max_seq_len, half), np.float32)
+        s = np.empty((self.cfg.max_seq_len, half), np.float32)
+        self._check(self.lib.slm_rope_tables_read(self._h, _fptr(c), _fptr(s)))
+        return c, s
+
+    def profile(self, enable: bool) -> None:
+        self._check(self.lib.slm_attn_profile(self._h, 1 if enable else 0))
+
+    def profile_read(self) -> dict:
+        arr = (_KernelStat * len(KERNEL_KINDS))()
+        self._check(self.lib.slm_attn_profile_read(self._h, arr))
+        return {name: (int(arr[i].launches), float(arr[i].total_ms))
+                for i, name in enumerate(KERNEL_KINDS)}
+
+    def decode_splits(self, seq_len: int) -> tuple[int, int]:
+        ns, ch = _I(), _I()
+        self._check(self.lib.slm_attn_decode_splits(self._h, seq_len, ctypes.byref(ns),
+                                                    ctypes.byref(ch)))
+        return ns.value, ch.value
+
+
+def header_functions(header: os.PathLike | str = HEADER_PATH) -> list[str]:
+    """Names of the functions include/slm_attn.h declares."""
+    import re
+
+    text = Path(header).read_text()
+    return sorted(set(re.findall(r"\b(slm_[a-z0-9_]+)\s*\(", text)))

@@ -1,0 +1,692 @@
+// Host side of the slm_attn C ABI: context, argument checks that mirror the
+// reference's asserts, RoPE tables, device KV region and kernel dispatch.
+#include "../../include/slm_attn.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "slm_internal.h"
+
+struct slm_attn_ctx {
+    slm_attn_config cfg{};
+    slm::Shape shape{};
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    // [num_layers][2][max_seq_len][kv_dim] f32, the arena's KV slices in order
+    float* kv = nullptr;
+    size_t kv_floats = 0;
+    // RoPE tables [max_seq_len][head_dim/2]
+    float* cos_t = nullptr;
+    float* sin_t = nullptr;
+    // split-K partials of one decode row
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    int max_splits = 1;
+    // staging for the host-pointer entry points
+    float* stage = nullptr;
+    size_t stage_floats = 0;
+    // kernel timing
+    bool profiling = false;
+    struct Pending {
+        int kind;
+        hipEvent_t begin;
+        hipEvent_t end;
+    };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> spare_events;
+    slm_kernel_stat stats[SLM_K_COUNT]{};
+    std::string err;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(slm_attn_ctx* c, int code, const std::string& msg) {
+    g_last_error = msg;
+    if (c) c->err = msg;
+    return code;
+}
+
+int hip_fail(slm_attn_ctx* c, hipError_t e, const char* what) {
+    return fail(c, SLM_ERR_HIP,
+                std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define SLM_HIP(c, expr)                                   \
+    do {                                                   \
+        hipError_t e_ = (expr);                            \
+        if (e_ != hipSuccess) return hip_fail(c, e_, #expr); \
+    } while (0)
+
+// LayerWorkspace::allocate asserts (transformer.rs:81-101).
+int validate(const slm_attn_config* cfg, std::string* why) {
+    if (!cfg) {
+        *why = "config is NULL";
+        return SLM_ERR_ARG;
+    }
+    if (cfg->num_heads <= 0 || cfg->num_kv_heads <= 0) {
+        *why = "num_heads and num_kv_heads must be positive";
+        return SLM_ERR_CONFIG;
+    }
+    if (cfg->dim <= 0 || cfg->dim % 32 != 0) {
+        *why = "dim must be a multiple of 32";
+        return SLM_ERR_CONFIG;
+    }
+    if (cfg->dim % cfg->num_heads != 0) {
+        *why = "dim must be divisible by num_heads";
+        return SLM_ERR_CONFIG;
+    }
+    if (cfg->num_heads % cfg->num_kv_heads != 0) {
+        *why = "num_heads must be divisible by num_kv_heads";
+        return SLM_ERR_CONFIG;
+    }
+    const int hd = cfg->dim / cfg->num_heads;
+    if (hd % 2 != 0) {
+        *why = "head_dim must be even for RoPE rotation";
+        return SLM_ERR_CONFIG;
+    }
+    if ((hd * cfg->num_kv_heads) % 32 != 0) {
+        *why = "kv_dim must be a multiple of 32";
+        return SLM_ERR_CONFIG;
+    }
+    if (cfg->max_seq_len <= 0 || cfg->num_layers <= 0) {
+        *why = "max_seq_len and num_layers must be positive";
+        return SLM_ERR_CONFIG;
+    }
+    if (!(cfg->rope_theta > 0.0f) || !isfinite(cfg->rope_theta)) {
+        *why = "rope_theta must be positive and finite";
+        return SLM_ERR_CONFIG;
+    }
+    const size_t kv_floats = (size_t)cfg->num_layers * 2 *
+                             (size_t)cfg->max_seq_len * (size_t)hd *
+                             (size_t)cfg->num_kv_heads;
+    if (kv_floats / 2 / (size_t)cfg->num_layers > (size_t)INT32_MAX * 4) {
+        *why = "KV region too large";
+        return SLM_ERR_CONFIG;
+    }
+    return SLM_OK;
+}
+
+// RoPE tables exactly as transformer.rs:124-133 computes them: f32 exponent
+// (2j)/hd, freq = 1 / theta^exponent through powf, angle = pos * freq in f32,
+// then sinf/cosf.  Host libm, never the device, so the tables are the
+// reference's own numbers.
+void rope_tables(int hd, int msl, float theta, std::vector<float>* cos_out,
+                 std::vector<float>* sin_out) {
+    const int half = hd / 2;
+    const float hd_f = (float)hd;
+    std::vector<float> freq(half);
+    for (int j = 0; j < half; ++j) {
+        const float expo = (float)(2 * j) / hd_f;
+        freq[j] = 1.0f / powf(theta, expo);
+    }
+    cos_out->resize((size_t)msl * half);
+    sin_out->resize((size_t)msl * half);
+    for (int pos = 0; pos < msl; ++pos) {
+        const float pos_f = (float)pos;
+        for (int j = 0; j < half; ++j) {
+            const float a = pos_f * freq[j];
+            (*cos_out)[(size_t)pos * half + j] = cosf(a);
+            (*sin_out)[(size_t)pos * half + j] = sinf(a);
+        }
+    }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
+    const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+    return a0 < b0 + b_bytes && b0 < a0 + a_bytes;
+}
+
+hipEvent_t take_event(slm_attn_ctx* c) {
+    if (!c->spare_events.empty()) {
+        hipEvent_t e = c->spare_events.back();
+        c->spare_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Brackets one kernel launch with events while profiling is on.
+struct Timed {
+    slm_attn_ctx* c;
+    int kind;
+    hipEvent_t b = nullptr;
+    hipEvent_t e = nullptr;
+    Timed(slm_attn_ctx* ctx, int k) : c(ctx), kind(k) {
+        if (!c->profiling) return;
+        b = take_event(c);
+        e = take_event(c);
+        if (b && e && hipEventRecord(b, c->stream) != hipSuccess) drop();
+    }
+    void done() {
+        if (!b || !e) return;
+        if (hipEventRecord(e, c->stream) != hipSuccess) {
+            drop();
+            return;
+        }
+        c->pending.push_back({kind, b, e});
+        b = e = nullptr;
+    }
+    // A launch whose events could not be recorded is left out of the stats.
+    void drop() {
+        if (b) c->spare_events.push_back(b);
+        if (e) c->spare_events.push_back(e);
+        b = e = nullptr;
+    }
+};
+
+float* k_base(slm_attn_ctx* c, int layer) {
+    return c->kv + (size_t)(2 * layer) * c->cfg.max_seq_len * c->shape.kv_dim;
+}
+float* v_base(slm_attn_ctx* c, int layer) {
+    return c->kv +
+           (size_t)(2 * layer + 1) * c->cfg.max_seq_len * c->shape.kv_dim;
+}
+
+int check_layer(slm_attn_ctx* c, int layer) {
+    if (layer < 0 || layer >= c->cfg.num_layers)
+        return fail(c, SLM_ERR_LAYER, "layer index out of range");
+    return SLM_OK;
+}
+
+int check_pos(slm_attn_ctx* c, int pos) {
+    if (pos < 0 || pos >= c->cfg.max_seq_len)
+        return fail(c, SLM_ERR_POS, "sequence position out of bounds");
+    return SLM_OK;
+}
+
+int check_batch(slm_attn_ctx* c, int start, int n) {
+    if (n <= 0 || start < 0 || (long)start + n > c->cfg.max_seq_len)
+        return fail(c, SLM_ERR_BATCH,
+                    "batch must be non-empty and start + n <= max_seq_len");
+    return SLM_OK;
+}
+
+int check_dev_ptrs(slm_attn_ctx* c, std::initializer_list<const void*> ps) {
+    for (const void* p : ps) {
+        if (!p) return fail(c, SLM_ERR_ARG, "NULL buffer");
+        if (!aligned16(p))
+            return fail(c, SLM_ERR_ARG, "device buffers must be 16-byte aligned");
+    }
+    return SLM_OK;
+}
+
+// out must not alias an input or the KV region (arena.rs:272-280).
+int check_out_alias(slm_attn_ctx* c, const float* out, size_t out_floats,
+                    std::initializer_list<std::pair<const float*, size_t>> ins,
+                    bool device) {
+    for (const auto& in : ins)
+        if (in.first && overlaps(out, out_floats * 4, in.first, in.second * 4))
+            return fail(c, SLM_ERR_ALIAS,
+                        "out must not overlap q, k, v or the KV cache");
+    if (device && overlaps(out, out_floats * 4, c->kv, c->kv_floats * 4))
+        return fail(c, SLM_ERR_ALIAS,
+                    "out must not overlap q, k, v or the KV cache");
+    return SLM_OK;
+}
+
+int launch_status(slm_attn_ctx* c, hipError_t e, const char* what) {
+    if (e != hipSuccess) return hip_fail(c, e, what);
+    return SLM_OK;
+}
+
+int do_append(slm_attn_ctx* c, int layer, int pos0, int n, const float* k,
+              const float* v) {
+    Timed t(c, SLM_K_APPEND);
+    hipError_t e = slm::launch_kv_append(c->shape, k, v, k_base(c, layer),
+                                         v_base(c, layer), c->cos_t, c->sin_t,
+                                         pos0, n, c->stream);
+    t.done();
+    return launch_status(c, e, "kv_append kernel launch");
+}
+
+// Attention of rows b < n at positions start + b over cache rows 0..start+b.
+// rotate: q is un-rotated and the kernels apply RoPE at each row's position.
+int do_attend(slm_attn_ctx* c, int layer, int start, int n, const float* q,
+              float* out, bool rotate) {
+    const slm::Shape& s = c->shape;
+    if (n > 1 && slm::prefill_mfma_supported(s)) {
+        slm::PrefillArgs pa{q,          k_base(c, layer), v_base(c, layer),
+                            rotate ? c->cos_t : nullptr,
+                            rotate ? c->sin_t : nullptr, out, start, n};
+        Timed t(c, SLM_K_PREFILL);
+        hipError_t e = slm::launch_prefill_mfma(s, pa, c->stream);
+        t.done();
+        return launch_status(c, e, "prefill kernel launch");
+    }
+    if (n == 1) {
+        int ns = 1, chunk = 1;
+        slm::decode_split_policy(s, start + 1, &ns, &chunk);
+        slm::RowsArgs a{q,      k_base(c, layer),
+                        v_base(c, layer),
+                        rotate ? c->cos_t : nullptr,
+                        rotate ? c->sin_t : nullptr,
+                        out,    c->part_o,
+                        c->part_ml,
+                        start,  1,
+                        chunk,  ns};
+        {
+            Timed t(c, SLM_K_DECODE_SPLIT);
+            hipError_t e = slm::launch_attn_rows(s, a, c->stream);
+            t.done();
+            if (e != hipSuccess) return hip_fail(c, e, "decode kernel launch");
+        }
+        if (ns > 1) {
+            Timed t(c, SLM_K_DECODE_COMBINE);
+            hipError_t e = slm::launch_attn_combine(s, a, c->stream);
+            t.done();
+            if (e != hipSuccess)
+                return hip_fail(c, e, "decode combine kernel launch");
+        }
+        return SLM_OK;
+    }
+    // Rows kernel with one split per row: each workgroup walks its row's
+    // whole causal range and writes the normalised output.
+    const int kMaxRows = 65535;
+    for (int b0 = 0; b0 < n; b0 += kMaxRows) {
+        const int nb = (n - b0 < kMaxRows) ? n - b0 : kMaxRows;
+        slm::RowsArgs a{q + (size_t)b0 * s.dim,
+                        k_base(c, layer),
+                        v_base(c, layer),
+                        rotate ? c->cos_t : nullptr,
+                        rotate ? c->sin_t : nullptr,
+                        out + (size_t)b0 * s.dim,
+                        nullptr,
+                        nullptr,
+                        start + b0,
+                        nb,
+                        c->cfg.max_seq_len,
+                        1};
+        Timed t(c, SLM_K_PREFILL);
+        hipError_t e = slm::launch_attn_rows(s, a, c->stream);
+        t.done();
+        if (e != hipSuccess) return hip_fail(c, e, "prefill kernel launch");
+    }
+    return SLM_OK;
+}
+
+int ensure_stage(slm_attn_ctx* c, size_t floats) {
+    if (c->stage_floats >= floats) return SLM_OK;
+    if (c->stage) {
+        SLM_HIP(c, hipStreamSynchronize(c->stream));
+        SLM_HIP(c, hipFree(c->stage));
+        c->stage = nullptr;
+        c->stage_floats = 0;
+    }
+    SLM_HIP(c, hipMalloc(&c->stage, floats * sizeof(float)));
+    c->stage_floats = floats;
+    return SLM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* slm_attn_version(void) { return "slm_attn 0.1 gfx950"; }
+
+const char* slm_attn_last_error(const slm_attn_ctx* ctx) {
+    return ctx ? ctx->err.c_str() : g_last_error.c_str();
+}
+
+int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
+    if (!out) return fail(nullptr, SLM_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    std::string why;
+    int rc = validate(cfg, &why);
+    if (rc != SLM_OK) return fail(nullptr, rc, why);
+    const int hd = cfg->dim / cfg->num_heads;
+    if (!slm::head_dim_supported(hd))
+        return fail(nullptr, SLM_ERR_UNSUPPORTED,
+                    "head_dim " + std::to_string(hd) +
+                        " is not compiled (16, 32, 48, 64, 96, 128, 256)");
+
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return fail(nullptr, SLM_ERR_DEVICE,
+                    std::string("no HIP device: ") + hipGetErrorString(e));
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess)
+        return fail(nullptr, SLM_ERR_DEVICE,
+                    std::string("hipGetDeviceProperties: ") +
+                        hipGetErrorString(e));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, SLM_ERR_DEVICE,
+                    std::string("device is ") + prop.gcnArchName +
+                        ", this library is built for gfx950 only");
+
+    slm_attn_ctx* c = new slm_attn_ctx();
+    c->cfg = *cfg;
+    c->device = dev;
+    slm::Shape& s = c->shape;
+    s.dim = cfg->dim;
+    s.num_heads = cfg->num_heads;
+    s.num_kv_heads = cfg->num_kv_heads;
+    s.head_dim = hd;
+    s.kv_dim = hd * cfg->num_kv_heads;
+    s.kv_mul = cfg->num_heads / cfg->num_kv_heads;
+    s.half = hd / 2;
+    s.max_seq_len = cfg->max_seq_len;
+
+    auto bail = [&](int code) {
+        slm_attn_destroy(c);
+        return code;
+    };
+    e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return bail(hip_fail(nullptr, e, "hipStreamCreate"));
+    c->stream = c->own_stream;
+
+    c->kv_floats = (size_t)cfg->num_layers * 2 * (size_t)cfg->max_seq_len *
+                   (size_t)s.kv_dim;
+    e = hipMalloc(&c->kv, c->kv_floats * sizeof(float));
+    if (e != hipSuccess) return bail(hip_fail(nullptr, e, "hipMalloc(KV region)"));
+    e = hipMemset(c->kv, 0, c->kv_floats * sizeof(float));
+    if (e != hipSuccess) return bail(hip_fail(nullptr, e, "hipMemset(KV region)"));
+
+    std::vector<float> ct, st;
+    rope_tables(hd, cfg->max_seq_len, cfg->rope_theta, &ct, &st);
+    const size_t tbytes = ct.size() * sizeof(float);
+    e = hipMalloc(&c->cos_t, tbytes);
+    if (e == hipSuccess) e = hipMalloc(&c->sin_t, tbytes);
+    if (e == hipSuccess)
+        e = hipMemcpy(c->cos_t, ct.data(), tbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(c->sin_t, st.data(), tbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return bail(hip_fail(nullptr, e, "RoPE table upload"));
+
+    int max_splits = 1;
+    for (int len = 1; len <= cfg->max_seq_len; ++len) {
+        int ns = 1, chunk = 1;
+        slm::decode_split_policy(s, len, &ns, &chunk);
+        if (ns > max_splits) max_splits = ns;
+    }
+    c->max_splits = max_splits;
+    e = hipMalloc(&c->part_o,
+                  (size_t)max_splits * s.num_heads * hd * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMalloc(&c->part_ml,
+                      (size_t)max_splits * s.num_heads * 2 * sizeof(float));
+    if (e != hipSuccess) return bail(hip_fail(nullptr, e, "hipMalloc(partials)"));
+
+    *out = c;
+    return SLM_OK;
+}
+
+void slm_attn_destroy(slm_attn_ctx* c) {
+    if (!c) return;
+    // Teardown is best effort: errors here have no caller to report to.
+    if (c->own_stream) (void)hipStreamSynchronize(c->own_stream);
+    if (c->stream && c->stream != c->own_stream)
+        (void)hipStreamSynchronize(c->stream);
+    for (auto& p : c->pending) {
+        (void)hipEventDestroy(p.begin);
+        (void)hipEventDestroy(p.end);
+    }
+    for (hipEvent_t e : c->spare_events) (void)hipEventDestroy(e);
+    (void)hipFree(c->kv);
+    (void)hipFree(c->cos_t);
+    (void)hipFree(c->sin_t);
+    (void)hipFree(c->part_o);
+    (void)hipFree(c->part_ml);
+    (void)hipFree(c->stage);
+    if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+    delete c;
+}
+
+int slm_attn_set_stream(slm_attn_ctx* c, void* stream) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    c->stream = stream ? (hipStream_t)stream : c->own_stream;
+    return SLM_OK;
+}
+
+void* slm_attn_get_stream(const slm_attn_ctx* c) {
+    return c ? (void*)c->stream : nullptr;
+}
+
+int slm_attn_sync(slm_attn_ctx* c) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
+    return SLM_OK;
+}
+
+int slm_kv_append_dev(slm_attn_ctx* c, int32_t layer, int32_t pos0, int32_t n,
+                      const float* k, const float* v) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_batch(c, pos0, n)) ||
+        (rc = check_dev_ptrs(c, {k, v})))
+        return rc;
+    return do_append(c, layer, pos0, n, k, v);
+}
+
+int slm_rope_apply_dev(slm_attn_ctx* c, float* x, int32_t n, int32_t row_len,
+                       int32_t pos0) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_batch(c, pos0, n)) || (rc = check_dev_ptrs(c, {x})))
+        return rc;
+    if (row_len <= 0 || row_len % c->shape.head_dim != 0)
+        return fail(c, SLM_ERR_ARG, "row_len must be a multiple of head_dim");
+    Timed t(c, SLM_K_ROPE);
+    hipError_t e = slm::launch_rope(c->shape, x, n, row_len, pos0, c->cos_t,
+                                    c->sin_t, c->stream);
+    t.done();
+    return launch_status(c, e, "rope kernel launch");
+}
+
+int slm_attn_attend_dev(slm_attn_ctx* c, int32_t layer, int32_t pos,
+                        const float* q_rot, float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_pos(c, pos)) ||
+        (rc = check_dev_ptrs(c, {q_rot, out})) ||
+        (rc = check_out_alias(c, out, c->shape.dim, {{q_rot, c->shape.dim}},
+                              true)))
+        return rc;
+    return do_attend(c, layer, pos, 1, q_rot, out, false);
+}
+
+int slm_attn_attend_batch_dev(slm_attn_ctx* c, int32_t layer, int32_t start,
+                              int32_t n, const float* q_rot, float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    const size_t rows = (size_t)(n > 0 ? n : 0) * c->shape.dim;
+    if ((rc = check_layer(c, layer)) || (rc = check_batch(c, start, n)) ||
+        (rc = check_dev_ptrs(c, {q_rot, out})) ||
+        (rc = check_out_alias(c, out, rows, {{q_rot, rows}}, true)))
+        return rc;
+    return do_attend(c, layer, start, n, q_rot, out, false);
+}
+
+int slm_attn_decode_dev(slm_attn_ctx* c, int32_t layer, int32_t pos,
+                        const float* q, const float* k, const float* v,
+                        float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    const slm::Shape& s = c->shape;
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_pos(c, pos)) ||
+        (rc = check_dev_ptrs(c, {q, k, v, out})) ||
+        (rc = check_out_alias(c, out, s.dim,
+                              {{q, s.dim}, {k, s.kv_dim}, {v, s.kv_dim}},
+                              true)))
+        return rc;
+    if ((rc = do_append(c, layer, pos, 1, k, v))) return rc;
+    return do_attend(c, layer, pos, 1, q, out, true);
+}
+
+int slm_attn_prefill_dev(slm_attn_ctx* c, int32_t layer, int32_t start,
+                         int32_t n, const float* q, const float* k,
+                         const float* v, float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    const slm::Shape& s = c->shape;
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_batch(c, start, n)) ||
+        (rc = check_dev_ptrs(c, {q, k, v, out})))
+        return rc;
+    const size_t qn = (size_t)n * s.dim, kn = (size_t)n * s.kv_dim;
+    if ((rc = check_out_alias(c, out, qn, {{q, qn}, {k, kn}, {v, kn}}, true)))
+        return rc;
+    if ((rc = do_append(c, layer, start, n, k, v))) return rc;
+    return do_attend(c, layer, start, n, q, out, true);
+}
+
+int slm_attn_decode(slm_attn_ctx* c, int32_t layer, int32_t pos, const float* q,
+                    const float* k, const float* v, float* out) {
+    return slm_attn_prefill(c, layer, pos, 1, q, k, v, out);
+}
+
+int slm_attn_prefill(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t n,
+                     const float* q, const float* k, const float* v,
+                     float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    const slm::Shape& s = c->shape;
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_batch(c, start, n)))
+        return rc;
+    if (!q || !k || !v || !out) return fail(c, SLM_ERR_ARG, "NULL buffer");
+    const size_t qn = (size_t)n * s.dim, kn = (size_t)n * s.kv_dim;
+    if ((rc = check_out_alias(c, out, qn, {{q, qn}, {k, kn}, {v, kn}}, false)))
+        return rc;
+    // staging: q | k | v | out, each segment 16-byte aligned (dim and kv_dim
+    // are multiples of 32 floats)
+    if ((rc = ensure_stage(c, 2 * qn + 2 * kn))) return rc;
+    float* dq = c->stage;
+    float* dk = dq + qn;
+    float* dv = dk + kn;
+    float* dout = dv + kn;
+    SLM_HIP(c, hipMemcpyAsync(dq, q, qn * 4, hipMemcpyHostToDevice, c->stream));
+    SLM_HIP(c, hipMemcpyAsync(dk, k, kn * 4, hipMemcpyHostToDevice, c->stream));
+    SLM_HIP(c, hipMemcpyAsync(dv, v, kn * 4, hipMemcpyHostToDevice, c->stream));
+    if (n == 1)
+        rc = slm_attn_decode_dev(c, layer, start, dq, dk, dv, dout);
+    else
+        rc = slm_attn_prefill_dev(c, layer, start, n, dq, dk, dv, dout);
+    if (rc) return rc;
+    SLM_HIP(c, hipMemcpyAsync(out, dout, qn * 4, hipMemcpyDeviceToHost,
+                              c->stream));
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
+    return SLM_OK;
+}
+
+int slm_kv_write(slm_attn_ctx* c, int32_t layer, int32_t which, int32_t pos0,
+                 int32_t n, const float* rows) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (which != 0 && which != 1) return fail(c, SLM_ERR_ARG, "which must be 0 or 1");
+    if (!rows || n <= 0 || pos0 < 0 || (long)pos0 + n > c->cfg.max_seq_len)
+        return fail(c, SLM_ERR_ARG, "row range outside the cache");
+    float* dst = (which ? v_base(c, layer) : k_base(c, layer)) +
+                 (size_t)pos0 * c->shape.kv_dim;
+    SLM_HIP(c, hipMemcpyAsync(dst, rows, (size_t)n * c->shape.kv_dim * 4,
+                              hipMemcpyHostToDevice, c->stream));
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
+    return SLM_OK;
+}
+
+int slm_kv_write_dev(slm_attn_ctx* c, int32_t layer, int32_t which,
+                     int32_t pos0, int32_t n, const float* rows) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (which != 0 && which != 1) return fail(c, SLM_ERR_ARG, "which must be 0 or 1");
+    if (!rows || n <= 0 || pos0 < 0 || (long)pos0 + n > c->cfg.max_seq_len)
+        return fail(c, SLM_ERR_ARG, "row range outside the cache");
+    const size_t bytes = (size_t)n * c->shape.kv_dim * 4;
+    if (overlaps(rows, bytes, c->kv, c->kv_floats * 4))
+        return fail(c, SLM_ERR_ALIAS, "source rows must not overlap the KV cache");
+    float* dst = (which ? v_base(c, layer) : k_base(c, layer)) +
+                 (size_t)pos0 * c->shape.kv_dim;
+    SLM_HIP(c, hipMemcpyAsync(dst, rows, bytes, hipMemcpyDeviceToDevice, c->stream));
+    return SLM_OK;
+}
+
+int slm_kv_read(slm_attn_ctx* c, int32_t layer, int32_t which, int32_t pos0,
+                int32_t n, float* rows) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (which != 0 && which != 1) return fail(c, SLM_ERR_ARG, "which must be 0 or 1");
+    if (!rows || n <= 0 || pos0 < 0 || (long)pos0 + n > c->cfg.max_seq_len)
+        return fail(c, SLM_ERR_ARG, "row range outside the cache");
+    const float* src = (which ? v_base(c, layer) : k_base(c, layer)) +
+                       (size_t)pos0 * c->shape.kv_dim;
+    SLM_HIP(c, hipMemcpyAsync(rows, src, (size_t)n * c->shape.kv_dim * 4,
+                              hipMemcpyDeviceToHost, c->stream));
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
+    return SLM_OK;
+}
+
+size_t slm_kv_offset(const slm_attn_ctx* c, int32_t layer, int32_t which,
+                     int32_t pos) {
+    if (!c || layer < 0 || layer >= c->cfg.num_layers || (which != 0 && which != 1) ||
+        pos < 0 || pos >= c->cfg.max_seq_len)
+        return (size_t)-1;
+    return ((size_t)(2 * layer + which) * c->cfg.max_seq_len + pos) *
+           c->shape.kv_dim;
+}
+
+float* slm_kv_device_ptr(const slm_attn_ctx* c) { return c ? c->kv : nullptr; }
+
+int slm_rope_tables_read(slm_attn_ctx* c, float* cos_out, float* sin_out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (!cos_out || !sin_out) return fail(c, SLM_ERR_ARG, "NULL buffer");
+    const size_t bytes = (size_t)c->cfg.max_seq_len * c->shape.half * 4;
+    SLM_HIP(c, hipMemcpyAsync(cos_out, c->cos_t, bytes, hipMemcpyDeviceToHost,
+                              c->stream));
+    SLM_HIP(c, hipMemcpyAsync(sin_out, c->sin_t, bytes, hipMemcpyDeviceToHost,
+                              c->stream));
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
+    return SLM_OK;
+}
+
+int slm_attn_profile(slm_attn_ctx* c, int32_t enable) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    c->profiling = enable != 0;
+    return SLM_OK;
+}
+
+int slm_attn_profile_read(slm_attn_ctx* c, slm_kernel_stat* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (!out) return fail(c, SLM_ERR_ARG, "NULL buffer");
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
+    for (auto& p : c->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.begin, p.end) == hipSuccess) {
+            c->stats[p.kind].launches += 1;
+            c->stats[p.kind].total_ms += ms;
+        }
+        c->spare_events.push_back(p.begin);
+        c->spare_events.push_back(p.end);
+    }
+    c->pending.clear();
+    for (int i = 0; i < SLM_K_COUNT; ++i) {
+        out[i] = c->stats[i];
+        c->stats[i] = slm_kernel_stat{};
+    }
+    return SLM_OK;
+}
+
+int slm_attn_decode_splits(const slm_attn_ctx* c, int32_t seq_len,
+                           int32_t* n_splits, int32_t* chunk) {
+    if (!c || !n_splits || !chunk || seq_len <= 0)
+        return fail(nullptr, SLM_ERR_ARG, "bad argument");
+    int ns = 1, ch = 1;
+    slm::decode_split_policy(c->shape, seq_len, &ns, &ch);
+    *n_splits = ns;
+    *chunk = ch;
+    return SLM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+// Internal interface between the C-ABI host code and the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace slm {
+
+// Shapes every kernel launch needs, derived from slm_attn_config exactly as
+// TransformerConfig::{head_dim, kv_dim, kv_mul} (transformer.rs:18-33).
+struct Shape {
+    int dim;
+    int num_heads;
+    int num_kv_heads;
+    int head_dim;
+    int kv_dim;
+    int kv_mul;
+    int half;  // head_dim / 2, the RoPE table row length
+    int max_seq_len;
+};
+
+// K/V append: rows pos0..pos0+n-1 of the layer's K slice get rope(k row),
+// the V slice gets the v row.  f32 products and sums rounded one by one.
+hipError_t launch_kv_append(const Shape& s, const float* k, const float* v,
+                            float* k_cache, float* v_cache, const float* cos_t,
+                            const float* sin_t, int pos0, int n,
+                            hipStream_t st);
+
+// In-place apply_rope_cached on n rows of row_len floats at pos0..pos0+n-1.
+hipError_t launch_rope(const Shape& s, float* x, int n, int row_len, int pos0,
+                       const float* cos_t, const float* sin_t, hipStream_t st);
+
+// Split-K attention over cache rows, one query row per blockIdx.z.
+struct RowsArgs {
+    const float* q;      // [rows][dim], head h at h*head_dim
+    const float* k_cache;  // layer K base, [max_seq_len][kv_dim]
+    const float* v_cache;  // layer V base
+    const float* cos_t;  // RoPE tables, or nullptr when q is already rotated
+    const float* sin_t;
+    float* out;          // [rows][dim], written when a row has one split
+    float* part_o;       // [rows][max_splits][num_heads][head_dim]
+    float* part_ml;      // [rows][max_splits][num_heads][2] (max, sum)
+    int start;           // row r sits at position start + r
+    int rows;
+    int chunk;           // positions per split
+    int max_splits;      // grid.x
+};
+
+// Chooses the decode split: n_splits and chunk as a pure function of
+// seq_len and the shape.  Also the positions one workgroup iteration covers.
+void decode_split_policy(const Shape& s, int seq_len, int* n_splits,
+                         int* chunk);
+int rows_iteration_span(const Shape& s);
+bool head_dim_supported(int head_dim);
+
+hipError_t launch_attn_rows(const Shape& s, const RowsArgs& a, hipStream_t st);
+hipError_t launch_attn_combine(const Shape& s, const RowsArgs& a,
+                               hipStream_t st);
+
+// Causal prefill on fp32 MFMA: rows b < n at positions start + b attend to
+// cache rows 0..start+b.  q is un-rotated when cos_t != nullptr.
+struct PrefillArgs {
+    const float* q;
+    const float* k_cache;
+    const float* v_cache;
+    const float* cos_t;
+    const float* sin_t;
+    float* out;
+    int start;
+    int n;
+};
+bool prefill_mfma_supported(const Shape& s);
+hipError_t launch_prefill_mfma(const Shape& s, const PrefillArgs& a,
+                               hipStream_t st);
+
+}  // namespace slm

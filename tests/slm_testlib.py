@@ -1,0 +1,147 @@
+"""Shared helpers for the tests: configs, seeded inputs, tolerance checks and
+loading of the product package (whose directory name has a hyphen)."""
+from __future__ import annotations
+
+import importlib.util
+import sys
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parents[1]
+if str(REPO) not in sys.path:
+    sys.path.insert(0, str(REPO))
+
+from oracle import py_oracle  # noqa: E402  (checker)
+
+# Tolerance of the parity bar: max-abs 1e-4 and max-rel 1e-3, the relative
+# error taken against max(|ref|, ATOL/RTOL) so that values near zero are held
+# to the absolute bound.  KV-cache rows are compared bit for bit.
+ATOL = 1e-4
+RTOL = 1e-3
+
+
+def load_product():
+    """Imports static-lm_amd/ as module `static_lm_amd`."""
+    name = "static_lm_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, REPO / "static-lm_amd" / "__init__.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    dim: int
+    num_heads: int
+    num_kv_heads: int
+    max_seq_len: int
+    num_layers: int
+    theta: float
+    prefill: int
+    decode: int
+    prefilled: int = 0  # rows written raw into the cache before the run
+    seed: int = 0
+
+    @property
+    def head_dim(self):
+        return self.dim // self.num_heads
+
+    @property
+    def kv_dim(self):
+        return self.head_dim * self.num_kv_heads
+
+    def cfg(self) -> py_oracle.Cfg:
+        return py_oracle.Cfg(self.dim, self.num_heads, self.num_kv_heads, self.max_seq_len,
+                             self.num_layers, self.theta)
+
+
+WORKLOADS = {
+    # the true built-in synthetic model of src/main.rs:266-274
+    "c0": Workload("synthetic-main", 256, 8, 2, 64, 2, 1e4, 16, 8, seed=0x5EED0000),
+    "c1": Workload("synthetic-256", 256, 4, 4, 512, 2, 1e4, 16, 8, seed=0x5EED0001),
+    "c2": Workload("stories15m", 288, 6, 6, 256, 6, 1e4, 16, 64, seed=0x5EED0002),
+    "c3": Workload("smollm2-135m", 576, 9, 3, 2048, 30, 1e5, 512, 256, seed=0x5EED0003),
+    "c4": Workload("llama3-8b", 4096, 32, 8, 8192, 1, 5e5, 4096, 128, seed=0x5EED0004),
+    "c5": Workload("llama3-8b-long", 4096, 32, 8, 131136, 1, 5e5, 0, 64, prefilled=131072,
+                   seed=0x5EED0005),
+    # shapes of the reference's own layer tests (transformer.rs:1000-1011, 1269-1278)
+    "ref_mha": Workload("ref-mha", 64, 4, 4, 8, 1, 1e4, 2, 2, seed=0x5EED0010),
+    "ref_gqa": Workload("ref-gqa", 64, 4, 2, 16, 2, 1e4, 4, 4, seed=0x5EED0011),
+}
+
+
+def gen(seed, shape) -> np.ndarray:
+    """Seeded N(0,1)*0.5 f32."""
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal(shape, dtype=np.float32) * np.float32(0.5)
+
+
+def layer_inputs(w: Workload, layer: int):
+    rows = w.prefill + w.decode
+    q = gen([w.seed, layer, 0], (rows, w.dim))
+    k = gen([w.seed, layer, 1], (rows, w.kv_dim))
+    v = gen([w.seed, layer, 2], (rows, w.kv_dim))
+    return q, k, v
+
+
+def prefilled_rows(w: Workload, layer: int, which: int, pos0: int, n: int) -> np.ndarray:
+    """Raw (already-final) cache rows for a pre-filled workload, by block of
+    4096 positions so any sub-range can be regenerated on its own."""
+    out = np.empty((n, w.kv_dim), np.float32)
+    blk = 4096
+    p = pos0
+    while p < pos0 + n:
+        b = p // blk
+        rows = gen([w.seed, layer, 10 + which, b], (blk, w.kv_dim))
+        lo = p - b * blk
+        take = min(blk - lo, pos0 + n - p)
+        out[p - pos0:p - pos0 + take] = rows[lo:lo + take]
+        p += take
+    return out
+
+
+def err_stats(got, ref, atol=ATOL, rtol=RTOL):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    diff = np.abs(got - ref)
+    rel = diff / np.maximum(np.abs(ref), atol / rtol)
+    return float(diff.max(initial=0.0)), float(rel.max(initial=0.0))
+
+
+def assert_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
+    got = np.asarray(got)
+    ref = np.asarray(ref)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite values"
+    mabs, mrel = err_stats(got, ref, atol, rtol)
+    assert mabs <= atol and mrel <= rtol, f"{what}: max-abs {mabs:.3e} max-rel {mrel:.3e}"
+
+
+def assert_bitwise(got, ref, what=""):
+    got = np.ascontiguousarray(got, np.float32)
+    ref = np.ascontiguousarray(ref, np.float32)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    neq = got.view(np.uint32) != ref.view(np.uint32)
+    assert not neq.any(), f"{what}: {int(neq.sum())} of {neq.size} words differ"
+
+
+def xorshift_f32(n: int, seed: int, lo: float, span: float) -> np.ndarray:
+    """The reference tests' pseudo_random_f32: xorshift32, unit = seed as f32 /
+    u32::MAX as f32, value = unit*span + lo in f32 (engine.rs:214-224 uses
+    span 4, lo -2)."""
+    out = np.empty(n, np.float32)
+    s = seed & 0xFFFFFFFF
+    umax = np.float32(4294967295.0)
+    for i in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        unit = np.float32(np.float32(s) / umax)
+        out[i] = np.float32(np.float32(unit * np.float32(span)) + np.float32(lo))
+    return out

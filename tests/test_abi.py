@@ -1,0 +1,68 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/slm_attn.h declares, and rejects bad arguments with the codes that
+mirror the reference's asserts before touching a device."""
+import ctypes
+import subprocess
+
+import pytest
+
+from slm_testlib import load_product
+
+P = load_product()
+
+
+def test_library_exports_every_header_function():
+    declared = P.header_functions()
+    assert len(declared) >= 20
+    lib = P.load_library()
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(P.SIGNATURES), "binding table out of step with the header"
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(P.LIB_PATH)], capture_output=True,
+                        text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in nm.splitlines() if " T " in ln}
+    assert set(declared) <= exported
+
+
+def test_version_and_null_handles():
+    lib = P.load_library()
+    assert b"gfx950" in lib.slm_attn_version()
+    assert lib.slm_attn_sync(None) == P.ERR_ARG
+    assert lib.slm_attn_decode(None, 0, 0, None, None, None, None) == P.ERR_ARG
+    assert lib.slm_attn_prefill_dev(None, 0, 0, 1, None, None, None, None) == P.ERR_ARG
+    assert lib.slm_kv_offset(None, 0, 0, 0) == ctypes.c_size_t(-1).value
+    assert lib.slm_kv_device_ptr(None) is None
+    lib.slm_attn_destroy(None)  # no-op
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads,msl,layers,theta,why", [
+    (250, 5, 5, 8, 1, 1e4, "dim must be a multiple of 32"),
+    (256, 3, 3, 8, 1, 1e4, "dim must be divisible by num_heads"),
+    (256, 8, 3, 8, 1, 1e4, "num_heads must be divisible by num_kv_heads"),
+    (96, 32, 32, 8, 1, 1e4, "head_dim must be even"),
+    (64, 4, 1, 8, 1, 1e4, "kv_dim must be a multiple of 32"),
+    (64, 4, 4, 0, 1, 1e4, "max_seq_len and num_layers must be positive"),
+    (64, 4, 4, 8, 0, 1e4, "max_seq_len and num_layers must be positive"),
+    (64, 4, 4, 8, 1, 0.0, "rope_theta"),
+    (64, 0, 0, 8, 1, 1e4, "num_heads and num_kv_heads must be positive"),
+])
+def test_create_rejects_configs_the_reference_asserts_on(dim, heads, kv_heads, msl, layers, theta,
+                                                         why):
+    with pytest.raises(P.SlmAttnError) as ei:
+        P.AttentionContext(dim, heads, kv_heads, msl, layers, theta)
+    assert ei.value.code == P.ERR_CONFIG
+    assert why in ei.value.message
+
+
+def test_create_rejects_uncompiled_head_dim():
+    # head_dim 40 satisfies every reference assert (dim 320, 8 heads) but has
+    # no compiled kernel
+    with pytest.raises(P.SlmAttnError) as ei:
+        P.AttentionContext(320, 8, 8, 16, 1)
+    assert ei.value.code == P.ERR_UNSUPPORTED
+
+
+def test_header_declares_error_codes_the_binding_uses():
+    text = P.HEADER_PATH.read_text()
+    for code, name in P.ERRORS.items():
+        assert f"#define {name} ({code})" in text

@@ -1,0 +1,316 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Bar: KV-cache rows and RoPE tables bit for bit; attention outputs within
+max-abs 1e-4 and max-rel 1e-3 (relative error floored at |ref| = 0.1).
+Small workloads run in full; the large ones (4096-row prefill, 131072-position
+decode) are checked on stated rows/steps with the oracle over the same cache,
+plus size-independent relations (prefill row == decode, split invariance,
+determinism).
+"""
+import os
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+import pytest
+
+from oracle import py_oracle as orc
+from slm_testlib import (WORKLOADS, assert_bitwise, assert_close, gen, layer_inputs,
+                         load_product, prefilled_rows)
+
+P = load_product()
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def make_ctx(w):
+    return P.AttentionContext(w.dim, w.num_heads, w.num_kv_heads, w.max_seq_len, w.num_layers,
+                              w.theta)
+
+
+@pytest.mark.parametrize("key", ["ref_mha", "ref_gqa", "c0", "c1", "c2"])
+def test_workload_full_parity(key):
+    w = WORKLOADS[key]
+    log(f"workload {key}: {w}")
+    cfg = w.cfg()
+    with make_ctx(w) as ctx:
+        om = orc.OracleModel(cfg)
+        c, s = ctx.rope_tables()
+        assert_bitwise(c, om.cos, "cos table")
+        assert_bitwise(s, om.sin, "sin table")
+        for layer in range(w.num_layers):
+            q, k, v = layer_inputs(w, layer)
+            n = w.prefill
+            g = ctx.prefill(layer, 0, q[:n], k[:n], v[:n])
+            r = om.prefill(layer, 0, q[:n], k[:n], v[:n])
+            assert_close(g, r, what=f"{key} layer {layer} prefill")
+            for st in range(w.decode):
+                p = n + st
+                g = ctx.decode(layer, p, q[p], k[p], v[p])
+                r = om.decode(layer, p, q[p], k[p], v[p])
+                assert_close(g, r, what=f"{key} layer {layer} decode pos {p}")
+            rows = n + w.decode
+            assert_bitwise(ctx.kv_read(layer, 0, 0, rows), om.k_cache(layer)[:rows], "K rows")
+            assert_bitwise(ctx.kv_read(layer, 1, 0, rows), om.v_cache(layer)[:rows], "V rows")
+
+
+def test_smollm2_shape_gqa3():
+    # SmolLM2-135M shape (9 heads over 3 KV heads, hd 64, theta 1e5): the first
+    # and last of its 30 layers, 512-row prefill then 256 decode steps
+    w = WORKLOADS["c3"]
+    cfg = w.cfg()
+    with make_ctx(w) as ctx:
+        om = orc.OracleModel(cfg)
+        for layer in (0, w.num_layers - 1):
+            log(f"c3 layer {layer}")
+            q, k, v = layer_inputs(w, layer)
+            n = w.prefill
+            g = ctx.prefill(layer, 0, q[:n], k[:n], v[:n])
+            r = om.prefill(layer, 0, q[:n], k[:n], v[:n])
+            assert_close(g, r, what=f"c3 layer {layer} prefill")
+            for st in range(w.decode):
+                p = n + st
+                g = ctx.decode(layer, p, q[p], k[p], v[p])
+                if st % 16 == 0 or st == w.decode - 1:
+                    r = om.decode(layer, p, q[p], k[p], v[p])
+                    assert_close(g, r, what=f"c3 layer {layer} decode pos {p}")
+                else:
+                    om.append(layer, p, k[p], v[p])
+            rows = n + w.decode
+            assert_bitwise(ctx.kv_read(layer, 0, 0, rows), om.k_cache(layer)[:rows], "K rows")
+            assert_bitwise(ctx.kv_read(layer, 1, 0, rows), om.v_cache(layer)[:rows], "V rows")
+
+
+def test_llama3_shape_prefill4096_then_decode():
+    w = WORKLOADS["c4"]
+    cfg = w.cfg()
+    q, k, v = layer_inputs(w, 0)
+    n = w.prefill
+    with make_ctx(w) as ctx:
+        log("c4 prefill 4096")
+        g = ctx.prefill(0, 0, q[:n], k[:n], v[:n])
+        om = orc.OracleModel(cfg)
+        om.append(0, 0, k[:n], v[:n])
+        assert_bitwise(ctx.kv_read(0, 0, 0, n), om.k_cache(0)[:n], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, n), om.v_cache(0)[:n], "V rows")
+        for b in (0, 1, 15, 16, 17, 63, 64, 127, 128, 255, 1000, 2047, 2048, 3333, 4095):
+            assert_close(g[b], om.attend(0, q[b], b), what=f"c4 prefill row {b}")
+        log("c4 decode 128")
+        for st in range(w.decode):
+            p = n + st
+            gd = ctx.decode(0, p, q[p], k[p], v[p])
+            om.append(0, p, k[p], v[p])
+            if st in (0, 1, 63, w.decode - 1):
+                assert_close(gd, om.attend(0, q[p], p), what=f"c4 decode pos {p}")
+        rows = n + w.decode
+        assert_bitwise(ctx.kv_read(0, 0, n, w.decode), om.k_cache(0)[n:rows], "K rows")
+
+
+def test_long_context_decode_131072():
+    w = WORKLOADS["c5"]
+    cfg = w.cfg()
+    q, k, v = layer_inputs(w, 0)
+    om = orc.OracleModel(cfg)
+    pre = w.prefilled
+    log("c5 prefill cache rows")
+    blk = 16384
+    with make_ctx(w) as ctx:
+        for p0 in range(0, pre, blk):
+            kr = prefilled_rows(w, 0, 0, p0, blk)
+            vr = prefilled_rows(w, 0, 1, p0, blk)
+            om.k_cache(0)[p0:p0 + blk] = kr
+            om.v_cache(0)[p0:p0 + blk] = vr
+            ctx.kv_write(0, 0, p0, kr)
+            ctx.kv_write(0, 1, p0, vr)
+        log("c5 decode 64 steps")
+        for st in range(w.decode):
+            p = pre + st
+            gd = ctx.decode(0, p, q[st], k[st], v[st])
+            if st in (0, w.decode - 1):
+                r = om.decode(0, p, q[st], k[st], v[st])
+                assert_close(gd, r, what=f"c5 decode pos {p}")
+            else:
+                om.append(0, p, k[st], v[st])
+        assert_bitwise(ctx.kv_read(0, 0, pre, w.decode), om.k_cache(0)[pre:pre + w.decode])
+        assert_bitwise(ctx.kv_read(0, 0, pre - 3, 3), om.k_cache(0)[pre - 3:pre])
+
+
+def test_prefill_rows_equal_sequential_decode_and_chunked_prefill():
+    # transformer.rs:1269-1358 relation, here elementwise: batched prefill rows
+    # equal token-by-token decode; a prefill continued at start > 0 equals one
+    # longer prefill; caches are bit-identical
+    w = WORKLOADS["c0"]
+    q, k, v = layer_inputs(w, 0)
+    n = 40
+    q, k, v = gen(7, (n, w.dim)), gen(8, (n, w.kv_dim)), gen(9, (n, w.kv_dim))
+    with make_ctx(w) as a, make_ctx(w) as b, make_ctx(w) as c:
+        ga = a.prefill(0, 0, q, k, v)
+        gb = np.stack([b.decode(0, p, q[p], k[p], v[p]) for p in range(n)])
+        assert_close(ga, gb, what="prefill vs decode")
+        c.prefill(0, 0, q[:13], k[:13], v[:13])
+        gc = c.prefill(0, 13, q[13:], k[13:], v[13:])
+        assert_close(gc, ga[13:], what="chunked prefill")
+        for ctx in (b, c):
+            assert_bitwise(ctx.kv_read(0, 0, 0, n), a.kv_read(0, 0, 0, n))
+            assert_bitwise(ctx.kv_read(0, 1, 0, n), a.kv_read(0, 1, 0, n))
+
+
+def test_decode_deterministic_and_split_invariant():
+    torch = pytest.importorskip("torch")
+    w = WORKLOADS["c4"]
+    pos = 6000
+    with make_ctx(w) as ctx:
+        ns, chunk = ctx.decode_splits(pos + 1)
+        log(f"splits at {pos + 1}: {ns} x {chunk}")
+        assert ns > 1
+        for p0 in range(0, pos + 1, 2048):
+            m = min(2048, pos + 1 - p0)
+            ctx.kv_write(0, 0, p0, gen([1, p0], (m, w.kv_dim)))
+            ctx.kv_write(0, 1, p0, gen([2, p0], (m, w.kv_dim)))
+        qd = torch.from_numpy(gen(3, w.dim)).cuda()
+        out1 = torch.empty(w.dim, device="cuda")
+        out2 = torch.empty(w.dim, device="cuda")
+        out3 = torch.empty(w.dim, device="cuda")
+        ctx.attend_dev(0, pos, qd.data_ptr(), out1.data_ptr())
+        ctx.attend_dev(0, pos, qd.data_ptr(), out2.data_ptr())
+        # one split per row: the prefill rows kernel over the same cache
+        ctx.attend_batch_dev(0, pos, 1, qd.data_ptr(), out3.data_ptr())
+        ctx.sync()
+        o1, o2, o3 = out1.cpu().numpy(), out2.cpu().numpy(), out3.cpu().numpy()
+        assert_bitwise(o1, o2, "repeat")
+        assert_close(o1, o3, what="split-K vs single split")
+        kc = ctx.kv_read(0, 0, 0, pos + 1)
+        vc = ctx.kv_read(0, 1, 0, pos + 1)
+        cfg = w.cfg()
+        kfull = np.zeros((cfg.max_seq_len, cfg.kv_dim), np.float32)
+        vfull = np.zeros_like(kfull)
+        kfull[:pos + 1], vfull[:pos + 1] = kc, vc
+        assert_close(o1, orc.attention(gen(3, w.dim), kfull, vfull, cfg, pos), what="vs oracle")
+
+
+def test_device_entry_points_match_oracle():
+    torch = pytest.importorskip("torch")
+    w = WORKLOADS["c1"]
+    cfg = w.cfg()
+    n = 24
+    q, k, v = gen(51, (n, w.dim)), gen(52, (n, w.kv_dim)), gen(53, (n, w.kv_dim))
+    om = orc.OracleModel(cfg)
+    with make_ctx(w) as ctx:
+        kd, vd = torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda()
+        ctx.kv_append_dev(1, 0, n, kd.data_ptr(), vd.data_ptr())
+        om.append(1, 0, k, v)
+        # apply_rope_cached on device rows, bit for bit
+        qd = torch.from_numpy(q).cuda()
+        ctx.rope_apply_dev(qd.data_ptr(), n, w.dim, 0)
+        ctx.sync()
+        q_rot = np.stack([om.rotated_q(q[b], b) for b in range(n)])
+        assert_bitwise(qd.cpu().numpy(), q_rot, "rope_apply_dev")
+        assert_bitwise(ctx.kv_read(1, 0, 0, n), om.k_cache(1)[:n], "kv_append_dev K")
+        assert_bitwise(ctx.kv_read(1, 1, 0, n), om.v_cache(1)[:n], "kv_append_dev V")
+        # causal_multi_head_attention_jit on the rotated q
+        out = torch.empty(w.dim, device="cuda")
+        ctx.attend_dev(1, n - 1, qd[n - 1].data_ptr(), out.data_ptr())
+        ctx.sync()
+        ref = orc.attention(q_rot[n - 1], om.k_cache(1), om.v_cache(1), cfg, n - 1)
+        assert_close(out.cpu().numpy(), ref, what="attend_dev")
+        # batched rows on rotated q
+        outb = torch.empty((n, w.dim), device="cuda")
+        ctx.attend_batch_dev(1, 0, n, qd.data_ptr(), outb.data_ptr())
+        ctx.sync()
+        for b in (0, 5, n - 1):
+            ref = orc.attention(q_rot[b], om.k_cache(1), om.v_cache(1), cfg, b)
+            assert_close(outb[b].cpu().numpy(), ref, what=f"attend_batch_dev row {b}")
+        # whole block on device pointers, on a caller-provided torch stream
+        s = torch.cuda.Stream()
+        ctx.set_stream(s.cuda_stream)
+        assert ctx.get_stream() == s.cuda_stream
+        q2, k2, v2 = gen(54, w.dim), gen(55, w.kv_dim), gen(56, w.kv_dim)
+        t = [torch.from_numpy(x).cuda() for x in (q2, k2, v2)]
+        torch.cuda.synchronize()
+        o = torch.empty(w.dim, device="cuda")
+        ctx.decode_dev(1, n, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), o.data_ptr())
+        s.synchronize()
+        ctx.set_stream(None)
+        assert_close(o.cpu().numpy(), om.decode(1, n, q2, k2, v2), what="decode_dev")
+
+
+def test_error_codes_mirror_reference_asserts():
+    torch = pytest.importorskip("torch")
+    w = WORKLOADS["c1"]
+    with make_ctx(w) as ctx:
+        q, k, v = gen(1, w.dim), gen(2, w.kv_dim), gen(3, w.kv_dim)
+        with pytest.raises(P.SlmAttnError) as e:
+            ctx.decode(0, w.max_seq_len, q, k, v)
+        assert e.value.code == P.ERR_POS
+        with pytest.raises(P.SlmAttnError) as e:
+            ctx.decode(w.num_layers, 0, q, k, v)
+        assert e.value.code == P.ERR_LAYER
+        with pytest.raises(P.SlmAttnError) as e:
+            ctx.prefill(0, w.max_seq_len - 2, np.tile(q, (3, 1)), np.tile(k, (3, 1)),
+                        np.tile(v, (3, 1)))
+        assert e.value.code == P.ERR_BATCH
+        buf = torch.zeros(4 * w.dim, device="cuda")
+        base = buf.data_ptr()
+        with pytest.raises(P.SlmAttnError) as e:  # out overlaps q
+            ctx.decode_dev(0, 0, base, base + 4 * w.dim, base + 8 * w.dim, base + 64)
+        assert e.value.code == P.ERR_ALIAS
+        with pytest.raises(P.SlmAttnError) as e:  # out inside the KV region
+            ctx.attend_dev(0, 0, base, ctx.kv_device_ptr())
+        assert e.value.code == P.ERR_ALIAS
+        with pytest.raises(P.SlmAttnError) as e:  # misaligned
+            ctx.attend_dev(0, 0, base + 4, base + 8 * w.dim)
+        assert e.value.code == P.ERR_ARG
+        with pytest.raises(P.SlmAttnError) as e:
+            ctx.kv_write(0, 2, 0, k)
+        assert e.value.code == P.ERR_ARG
+        assert ctx.kv_offset(1, 1, 3) == ((2 * 1 + 1) * w.max_seq_len + 3) * w.kv_dim
+        assert ctx.kv_offset(2, 0, 0) == 2**64 - 1
+        # the context still works after rejected calls
+        out = ctx.decode(0, 0, q, k, v)
+        assert_bitwise(out[:w.head_dim], v[:w.head_dim], "pos 0 output is V row 0")
+
+
+def test_profile_counts_launches():
+    w = WORKLOADS["c4"]
+    with make_ctx(w) as ctx:
+        ctx.profile(True)
+        q, k, v = gen(1, (64, w.dim)), gen(2, (64, w.kv_dim)), gen(3, (64, w.kv_dim))
+        ctx.prefill(0, 0, q, k, v)
+        for p in range(64, 66):
+            ctx.decode(0, p, q[0], k[0], v[0])
+        st = ctx.profile_read()
+        assert st["append"][0] == 3
+        assert st["prefill"][0] >= 1 and st["decode_split"][0] == 2
+        assert all(ms >= 0.0 for _, ms in st.values())
+        st2 = ctx.profile_read()
+        assert all(cnt == 0 for cnt, _ in st2.values())
+
+
+def test_cpp_host_mirror_binary():
+    exe = P.PKG_DIR / "slm_host_demo"
+    assert exe.exists(), "build the package first"
+    w = WORKLOADS["ref_gqa"]
+    cfg = w.cfg()
+    npf, nd = 9, 5
+    rows = npf + nd
+    q, k, v = gen(61, (rows, w.dim)), gen(62, (rows, w.kv_dim)), gen(63, (rows, w.kv_dim))
+    with tempfile.TemporaryDirectory() as td:
+        fin, fout = os.path.join(td, "in.bin"), os.path.join(td, "out.bin")
+        with open(fin, "wb") as f:
+            f.write(q.tobytes() + k.tobytes() + v.tobytes())
+        subprocess.run([str(exe), str(w.dim), str(w.num_heads), str(w.num_kv_heads),
+                        str(w.max_seq_len), str(w.theta), str(npf), str(nd), fin, fout],
+                       check=True, timeout=60)
+        raw = np.fromfile(fout, dtype=np.float32)
+    out = raw[:rows * w.dim].reshape(rows, w.dim)
+    err = raw[rows * w.dim:].view(np.int32)[0]
+    assert err == P.ERR_POS
+    om = orc.OracleModel(cfg)
+    ref = np.concatenate([om.prefill(0, 0, q[:npf], k[:npf], v[:npf]),
+                          np.stack([om.decode(0, p, q[p], k[p], v[p]) for p in range(npf, rows)])])
+    assert_close(out, ref, what="C++ host mirror")
