@@ -96,6 +96,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
     pos = ctx_len - 1
     ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, ctx_len, layers, THETA)
     stream = torch.cuda.current_stream()
+    assert stream.cuda_stream != 0, "run on a non-default stream"
     ctx.set_stream(stream.cuda_stream)
     fill_cache(torch, ctx, layers, ctx_len, ctx_len, 1234)
     q = torch.randn(layers, DIM, device="cuda") * 0.5
@@ -148,6 +149,7 @@ def bench_prefill_4k(torch, P, reps: int) -> dict:
     n, msl = 4096, 8192
     ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, msl, 1, THETA)
     stream = torch.cuda.current_stream()
+    assert stream.cuda_stream != 0, "run on a non-default stream"
     ctx.set_stream(stream.cuda_stream)
     q = torch.randn(n, DIM, device="cuda") * 0.5
     k = torch.randn(n, KV_DIM, device="cuda") * 0.5
@@ -185,6 +187,7 @@ def bench_decode_131k(torch, P) -> dict:
     msl = pre + steps
     ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, msl, 1, THETA)
     stream = torch.cuda.current_stream()
+    assert stream.cuda_stream != 0, "run on a non-default stream"
     ctx.set_stream(stream.cuda_stream)
     fill_cache(torch, ctx, 1, msl, pre, 99)
     q = torch.randn(steps, DIM, device="cuda") * 0.5
@@ -290,6 +293,10 @@ def main() -> int:
         return 1
     torch.manual_seed(0)
     log(f"device {torch.cuda.get_device_name(0)}")
+    # A dedicated stream: the legacy default stream's handle is 0, which the
+    # C ABI reads as "the context's own stream".  Every kernel of the library
+    # and every timing event goes on this one stream.
+    torch.cuda.set_stream(torch.cuda.Stream())
 
     log("decode @32k")
     d = bench_decode_32k(torch, P, args.steps, args.warmup)

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import sys
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -122,6 +123,28 @@ SIGNATURES = {
 _lib = None
 
 
+def _share_torch_hip_runtime() -> None:
+    """Maps PyTorch's bundled HIP runtime before ours, when torch is installed.
+
+    torch ships its own libamdhip64 (SONAME libamdhip64.so.7) and its
+    libc10_hip asks for it as "libamdhip64.so".  If this library were loaded
+    first, the system runtime would be mapped under the SONAME and torch would
+    later map a second HIP runtime that finds no GPU.  Mapping torch's copy
+    first makes our DT_NEEDED libamdhip64.so.7 resolve to it, so the process
+    has one runtime in either import order.  SLM_ATTN_SYSTEM_HIP=1 skips this.
+    """
+    if os.environ.get("SLM_ATTN_SYSTEM_HIP") == "1" or "torch" in sys.modules:
+        return
+    import importlib.util
+
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        return
+    hip = Path(spec.submodule_search_locations[0]) / "lib" / "libamdhip64.so"
+    if hip.exists():
+        ctypes.CDLL(str(hip), mode=ctypes.RTLD_GLOBAL)
+
+
 def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     """Loads libslm_attn.so; raises if it has not been built."""
     global _lib
@@ -132,6 +155,7 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
         raise FileNotFoundError(
             f"{p} is missing: build the HIP library first "
             "(python static-lm_amd/build.py or __graft_entry__.build())")
+    _share_torch_hip_runtime()
     lib = ctypes.CDLL(str(p))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

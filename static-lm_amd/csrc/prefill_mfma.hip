@@ -1,13 +1,333 @@
-// Causal prefill attention on fp32 MFMA for gfx950 (not yet enabled: the
-// split-K rows kernel serves prefill until this path is parity-checked).
+// Causal prefill attention on fp32 MFMA (v_mfma_f32_16x16x4_f32) for gfx950.
+//
+// Replaces the per-row loop of forward_batch_with_kv (transformer.rs:563-593),
+// where row b at position p = start + b attends to cache rows 0..p.
+//
+// Tiling.  A workgroup of HW*QS waves owns one query block and HW query heads
+// of one KV head (HW divides kv_mul), so every K/V tile staged in LDS serves
+// HW heads.  Each wave owns 16*NQT query rows of one head.  Keys stream
+// through LDS in tiles of 32 rows (row stride HD+4 floats against bank
+// conflicts); the next tile is prefetched into registers while the current
+// one is in use.
+//
+// Transposed products keep softmax state lane-local.  With the 16x16x4 MFMA
+// layout (lane l: A[l%16][l/16], B[l/16][l%16], D[4*(l/16)+r][l%16]):
+//   S^T = K . Q^T   A = K rows (keys) , B = Q^T (queries): lane l ends with
+//                   scores of query l%16 against keys 4*(l/16)+r;
+//   O^T = V^T . P^T A = V^T (head dims), B = P^T: k-step j of a 16-key block
+//                   uses key 4*(l/16)+j, which is exactly D register j of S^T,
+//                   so probabilities feed the second MFMA with no shuffle;
+//                   lane l accumulates O^T[d][query l%16].
+// The head dimension is split into four contiguous quarters, one per lane
+// group l/16, so Q and K fragments are contiguous (128-bit loads) and the
+// RoPE pairs of q stay inside one lane.
+//
+// Online softmax runs in the log2 domain (q pre-scaled by log2(e)/sqrt(hd));
+// the running max is reduced across the four lane groups each tile, the
+// running sum stays a per-lane partial until the end.
+#include <math.h>
+
 #include "slm_internal.h"
 
 namespace slm {
+namespace {
 
-bool prefill_mfma_supported(const Shape&) { return false; }
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-hipError_t launch_prefill_mfma(const Shape&, const PrefillArgs&, hipStream_t) {
-    return hipErrorNotSupported;
+constexpr int kKT = 32;  // keys per LDS tile
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float4 ld4(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+}
+
+struct PrefillParams {
+    const float* q;
+    const float* k_cache;
+    const float* v_cache;
+    const float* cos_t;
+    const float* sin_t;
+    float* out;
+    int start;
+    int n;
+    int dim;
+    int kv_dim;
+    int kv_mul;
+    int half;
+    float scale_log2;
+};
+
+// Two waves per SIMD let one wave's MFMAs overlap another's softmax; the
+// largest variants keep one wave per SIMD rather than spill.
+template <int HD, int HW>
+constexpr int prefill_waves_per_simd() {
+    return (HD > 128 || (HD == 128 && HW == 3)) ? 1 : 2;
+}
+
+template <int HD, int HW, int QS, int NQT>
+__global__ __launch_bounds__(64 * HW * QS, (prefill_waves_per_simd<HD, HW>())) void
+prefill_mfma_kernel(PrefillParams p) {
+    constexpr int NW = HW * QS;
+    constexpr int NT = 64 * NW;
+    constexpr int LDK = HD + 4;
+    constexpr int DPL = HD / 4;   // contiguous head dims per lane group
+    constexpr int NDT = HD / 16;  // 16-wide head-dim tiles of O^T
+    constexpr int QPW = 16 * NQT; // query rows per wave
+    constexpr int QB = QPW * QS;  // query rows per workgroup
+    constexpr int F4 = kKT * HD / 4;          // float4 per K (or V) tile
+    constexpr int NPF = (F4 + NT - 1) / NT;   // float4 per thread per tile
+    static_assert(DPL % 4 == 0 && HD % 16 == 0, "head_dim must be a multiple of 16");
+
+    __shared__ __align__(16) float sK[kKT * LDK];
+    __shared__ __align__(16) float sV[kKT * LDK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int hw = wave % HW;
+    const int qs = wave / HW;
+
+    const int n_qb = (p.n + QB - 1) / QB;
+    const int qb = n_qb - 1 - (int)blockIdx.x;  // longest causal ranges first
+    const int head = blockIdx.y * HW + hw;
+    const int g = (blockIdx.y * HW) / p.kv_mul;
+    const int q0 = qb * QB + qs * QPW;  // first query row of this wave
+    const int wg_rows = min(p.n - qb * QB, QB);
+    const int kv_len = p.start + qb * QB + wg_rows;  // keys 0..kv_len-1
+    const int n_tiles = (kv_len + kKT - 1) / kKT;
+    const int wave_rows = max(0, min(QPW, p.n - q0));
+    const int wave_last_pos = p.start + q0 + wave_rows - 1;
+
+    // Q fragments: row q0 + qt*16 + lr, dims lg*DPL .. +DPL, rotated, scaled.
+    float qf[NQT][DPL];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+        const int row = q0 + qt * 16 + lr;
+        const bool ok = row < p.n;
+        const float* src = p.q + (long)(ok ? row : 0) * p.dim + head * HD + lg * DPL;
+        const long tr = (long)(p.start + (ok ? row : 0)) * p.half + (lg * DPL >> 1);
+#pragma unroll
+        for (int c = 0; c < DPL / 4; ++c) {
+            float4 x = ok ? ld4(src + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p.cos_t != nullptr) {
+                const float c0 = p.cos_t[tr + 2 * c], s0 = p.sin_t[tr + 2 * c];
+                const float c1 = p.cos_t[tr + 2 * c + 1], s1 = p.sin_t[tr + 2 * c + 1];
+                const float x0 = x.x * c0 - x.y * s0, x1 = x.x * s0 + x.y * c0;
+                const float x2 = x.z * c1 - x.w * s1, x3 = x.z * s1 + x.w * c1;
+                x = make_float4(x0, x1, x2, x3);
+            }
+            qf[qt][4 * c + 0] = x.x * p.scale_log2;
+            qf[qt][4 * c + 1] = x.y * p.scale_log2;
+            qf[qt][4 * c + 2] = x.z * p.scale_log2;
+            qf[qt][4 * c + 3] = x.w * p.scale_log2;
+        }
+    }
+
+    floatx4 o[NQT][NDT];
+    float m[NQT], l[NQT];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const float* kg = p.k_cache + g * HD;
+    const float* vg = p.v_cache + g * HD;
+    float4 pk[NPF], pv[NPF];
+    auto prefetch = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < NPF; ++i) {
+            const int f = tid + i * NT;
+            const int key = kb + f / (HD / 4);
+            const int col = (f % (HD / 4)) * 4;
+            if (f < F4 && key < kv_len) {
+                pk[i] = ld4(kg + (long)key * p.kv_dim + col);
+                pv[i] = ld4(vg + (long)key * p.kv_dim + col);
+            } else {
+                pk[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                pv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
+    prefetch(0);
+
+    for (int it = 0; it < n_tiles; ++it) {
+        const int kb = it * kKT;
+        __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+        for (int i = 0; i < NPF; ++i) {
+            const int f = tid + i * NT;
+            if (f < F4) {
+                const int r = f / (HD / 4), col = (f % (HD / 4)) * 4;
+                *reinterpret_cast<float4*>(&sK[r * LDK + col]) = pk[i];
+                *reinterpret_cast<float4*>(&sV[r * LDK + col]) = pv[i];
+            }
+        }
+        __syncthreads();
+        if (it + 1 < n_tiles) prefetch(kb + kKT);
+        if (wave_rows == 0 || kb > wave_last_pos) continue;  // wave-uniform
+
+        // S^T tiles [key sub-tile][query tile]
+        floatx4 s[2][NQT];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int qt = 0; qt < NQT; ++qt) s[ks][qt] = floatx4{0.f, 0.f, 0.f, 0.f};
+            const float* krow = &sK[(ks * 16 + lr) * LDK + lg * DPL];
+#pragma unroll
+            for (int c = 0; c < DPL / 4; ++c) {
+                const float4 kf = ld4(krow + 4 * c);
+#pragma unroll
+                for (int qt = 0; qt < NQT; ++qt) {
+                    s[ks][qt] = mfma4(kf.x, qf[qt][4 * c + 0], s[ks][qt]);
+                    s[ks][qt] = mfma4(kf.y, qf[qt][4 * c + 1], s[ks][qt]);
+                    s[ks][qt] = mfma4(kf.z, qf[qt][4 * c + 2], s[ks][qt]);
+                    s[ks][qt] = mfma4(kf.w, qf[qt][4 * c + 3], s[ks][qt]);
+                }
+            }
+        }
+
+        // causal mask, online softmax
+        const bool diag = kb + kKT - 1 > p.start + q0;  // some key may be masked
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+            const int qpos = p.start + q0 + qt * 16 + lr;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = s[ks][qt][r];
+                    if (diag && kb + ks * 16 + 4 * lg + r > qpos) v = -INFINITY;
+                    s[ks][qt][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mn = fmaxf(m[qt], mx);
+            const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
+            m[qt] = mn;
+            float ps = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float e = __builtin_amdgcn_exp2f(s[ks][qt][r] - mn);
+                    s[ks][qt][r] = e;
+                    ps += e;
+                }
+            }
+            l[qt] = l[qt] * alpha + ps;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+        }
+
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float* vrow = &sV[(ks * 16 + 4 * lg + j) * LDK + lr];
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const float vf = vrow[dt * 16];
+#pragma unroll
+                    for (int qt = 0; qt < NQT; ++qt)
+                        o[qt][dt] = mfma4(vf, s[ks][qt][j], o[qt][dt]);
+                }
+            }
+        }
+    }
+
+    // normalise and store: lane holds out[row q0+qt*16+lr][dt*16 + 4*lg .. +3]
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+        float lt = l[qt];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        const int row = q0 + qt * 16 + lr;
+        if (row < p.n) {
+            const float inv = 1.0f / lt;
+            float* dst = p.out + (long)row * p.dim + head * HD + 4 * lg;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                float4 r;
+                r.x = o[qt][dt][0] * inv;
+                r.y = o[qt][dt][1] * inv;
+                r.z = o[qt][dt][2] * inv;
+                r.w = o[qt][dt][3] * inv;
+                *reinterpret_cast<float4*>(dst + dt * 16) = r;
+            }
+        }
+    }
+}
+
+struct Tiling {
+    int hw;
+    int qs;
+};
+
+Tiling pick_tiling(int kv_mul) {
+    if (kv_mul % 4 == 0) return {4, 1};
+    if (kv_mul % 3 == 0) return {3, 1};
+    if (kv_mul % 2 == 0) return {2, 2};
+    return {1, 4};
+}
+
+template <int HD, int HW, int QS>
+hipError_t launch_t(const Shape& s, const PrefillParams& pp, hipStream_t st) {
+    constexpr int NQT = HD > 128 ? 1 : 2;
+    constexpr int QB = 16 * NQT * QS;
+    const int n_qb = (pp.n + QB - 1) / QB;
+    const dim3 grid(n_qb, s.num_heads / HW);
+    hipLaunchKernelGGL((prefill_mfma_kernel<HD, HW, QS, NQT>), grid, dim3(64 * HW * QS), 0,
+                       st, pp);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
+    const Tiling t = pick_tiling(s.kv_mul);
+    if (t.hw == 4) return launch_t<HD, 4, 1>(s, pp, st);
+    if (t.hw == 3) return launch_t<HD, 3, 1>(s, pp, st);
+    if (t.hw == 2) return launch_t<HD, 2, 2>(s, pp, st);
+    return launch_t<HD, 1, 4>(s, pp, st);
+}
+
+}  // namespace
+
+bool prefill_mfma_supported(const Shape& s) {
+    switch (s.head_dim) {
+        case 16: case 32: case 48: case 64: case 96: case 128: case 256:
+            return true;
+        default:
+            return false;
+    }
+}
+
+hipError_t launch_prefill_mfma(const Shape& s, const PrefillArgs& a, hipStream_t st) {
+    PrefillParams pp{a.q,   a.k_cache, a.v_cache, a.cos_t,  a.sin_t, a.out, a.start,
+                     a.n,   s.dim,     s.kv_dim,  s.kv_mul, s.half,
+                     1.4426950408889634f / sqrtf((float)s.head_dim)};
+    if (a.n > 65535 * 64) return hipErrorInvalidValue;
+    switch (s.head_dim) {
+        case 16: return launch_hd<16>(s, pp, st);
+        case 32: return launch_hd<32>(s, pp, st);
+        case 48: return launch_hd<48>(s, pp, st);
+        case 64: return launch_hd<64>(s, pp, st);
+        case 96: return launch_hd<96>(s, pp, st);
+        case 128: return launch_hd<128>(s, pp, st);
+        case 256: return launch_hd<256>(s, pp, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace slm

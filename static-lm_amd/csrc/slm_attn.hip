@@ -543,6 +543,10 @@ int slm_attn_prefill_dev(slm_attn_ctx* c, int32_t layer, int32_t start,
 
 int slm_attn_decode(slm_attn_ctx* c, int32_t layer, int32_t pos, const float* q,
                     const float* k, const float* v, float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    // the decode asserts, in the reference's order (transformer.rs:404-407)
+    if ((rc = check_layer(c, layer)) || (rc = check_pos(c, pos))) return rc;
     return slm_attn_prefill(c, layer, pos, 1, q, k, v, out);
 }
 

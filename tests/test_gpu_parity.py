@@ -172,18 +172,19 @@ def test_decode_deterministic_and_split_invariant():
             m = min(2048, pos + 1 - p0)
             ctx.kv_write(0, 0, p0, gen([1, p0], (m, w.kv_dim)))
             ctx.kv_write(0, 1, p0, gen([2, p0], (m, w.kv_dim)))
-        qd = torch.from_numpy(gen(3, w.dim)).cuda()
+        q2 = torch.from_numpy(np.stack([gen(4, w.dim), gen(3, w.dim)])).cuda()
+        qd = q2[1]
         out1 = torch.empty(w.dim, device="cuda")
         out2 = torch.empty(w.dim, device="cuda")
-        out3 = torch.empty(w.dim, device="cuda")
+        out3 = torch.empty((2, w.dim), device="cuda")
         ctx.attend_dev(0, pos, qd.data_ptr(), out1.data_ptr())
         ctx.attend_dev(0, pos, qd.data_ptr(), out2.data_ptr())
-        # one split per row: the prefill rows kernel over the same cache
-        ctx.attend_batch_dev(0, pos, 1, qd.data_ptr(), out3.data_ptr())
+        # the same row through the prefill kernel (no split): rows at pos-1, pos
+        ctx.attend_batch_dev(0, pos - 1, 2, q2.data_ptr(), out3.data_ptr())
         ctx.sync()
-        o1, o2, o3 = out1.cpu().numpy(), out2.cpu().numpy(), out3.cpu().numpy()
+        o1, o2, o3 = out1.cpu().numpy(), out2.cpu().numpy(), out3[1].cpu().numpy()
         assert_bitwise(o1, o2, "repeat")
-        assert_close(o1, o3, what="split-K vs single split")
+        assert_close(o1, o3, what="split-K decode vs prefill row")
         kc = ctx.kv_read(0, 0, 0, pos + 1)
         vc = ctx.kv_read(0, 1, 0, pos + 1)
         cfg = w.cfg()
@@ -314,3 +315,36 @@ def test_cpp_host_mirror_binary():
     ref = np.concatenate([om.prefill(0, 0, q[:npf], k[:npf], v[:npf]),
                           np.stack([om.decode(0, p, q[p], k[p], v[p]) for p in range(npf, rows)])])
     assert_close(out, ref, what="C++ host mirror")
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads", [
+    (64, 4, 4),      # hd 16, MHA (the reference's layer test shape)
+    (256, 8, 2),     # hd 32, kv_mul 4
+    (288, 6, 6),     # hd 48
+    (576, 9, 3),     # hd 64, kv_mul 3
+    (512, 8, 4),     # hd 64, kv_mul 2
+    (768, 8, 8),     # hd 96
+    (2048, 16, 2),   # hd 128, kv_mul 8
+    (1024, 4, 4),    # hd 256
+])
+@pytest.mark.parametrize("start,n", [(0, 2), (0, 37), (0, 130), (50, 5), (61, 67)])
+def test_prefill_shapes_and_ragged_batches(dim, heads, kv_heads, start, n):
+    msl = 200
+    cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, 1e4)
+    log(f"prefill shape dim {dim} heads {heads}/{kv_heads} start {start} n {n}")
+    kvd = cfg.kv_dim
+    q = gen([71, dim, n], (start + n, dim))
+    k = gen([72, dim, n], (start + n, kvd))
+    v = gen([73, dim, n], (start + n, kvd))
+    om = orc.OracleModel(cfg)
+    with P.AttentionContext(dim, heads, kv_heads, msl, 1) as ctx:
+        if start:
+            ctx.prefill(0, 0, q[:start], k[:start], v[:start])
+            om.append(0, 0, k[:start], v[:start])
+        g = ctx.prefill(0, start, q[start:], k[start:], v[start:])
+        om.append(0, start, k[start:], v[start:])
+        assert_bitwise(ctx.kv_read(0, 0, 0, start + n), om.k_cache(0)[:start + n], "K rows")
+        for b in sorted({0, 1, n // 2, n - 1}):
+            if b < n:
+                assert_close(g[b], om.attend(0, q[start + b], start + b),
+                             what=f"row {b} at {start + b}")
