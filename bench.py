@@ -128,7 +128,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
         step()
     prof = ctx.profile_read()
     ctx.profile(False)
-    n_split, split_ms = prof["decode_split"]
+    n_split, split_ms = prof["decode"]
     avg_split_s = split_ms / max(n_split, 1) / 1e3
     kv_bytes = 2 * (pos + 1) * KV_DIM * 4
     achieved = kv_bytes / avg_split_s / 1e9

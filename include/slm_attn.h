@@ -176,12 +176,11 @@ int slm_rope_tables_read(slm_attn_ctx* ctx, float* cos_out, float* sin_out);
  * of launches and their summed duration in ms (it synchronizes the stream).
  * Reading resets the counters. */
 enum {
-    SLM_K_APPEND = 0,       /* rope + KV append */
-    SLM_K_DECODE_SPLIT = 1, /* split-K decode attention */
-    SLM_K_DECODE_COMBINE = 2,
-    SLM_K_PREFILL = 3,      /* causal prefill attention */
-    SLM_K_ROPE = 4,         /* standalone rope */
-    SLM_K_COUNT = 5
+    SLM_K_APPEND = 0,  /* rope(k) + KV append of a prefill batch */
+    SLM_K_DECODE = 1,  /* fused decode: append + split-K attention + merge */
+    SLM_K_PREFILL = 2, /* causal prefill attention */
+    SLM_K_ROPE = 3,    /* standalone rope */
+    SLM_K_COUNT = 4
 };
 typedef struct slm_kernel_stat {
     int64_t launches;

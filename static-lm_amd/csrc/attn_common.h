@@ -1,0 +1,183 @@
+// Device helpers shared by the attention kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+namespace slm {
+
+typedef float vfloat4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld4(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+}
+
+// K/V rows are read once per step: nontemporal loads keep them from evicting
+// what is reused (streaming reads measured ~15% faster this way on MI355X).
+__device__ __forceinline__ float4 ld4_stream(const float* p) {
+    const vfloat4 v = __builtin_nontemporal_load(reinterpret_cast<const vfloat4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// One RoPE pair exactly as apply_rope_cached computes it
+// (transformer.rs:186-191): every product and sum rounded on its own.
+__device__ __forceinline__ float2 rope_pair_exact(float2 x, float c, float s) {
+#pragma clang fp contract(off)
+    const float t0 = x.x * c;
+    const float t1 = x.y * s;
+    const float t2 = x.x * s;
+    const float t3 = x.y * c;
+    float2 r;
+    r.x = t0 - t1;
+    r.y = t2 + t3;
+    return r;
+}
+
+// Two consecutive pairs (x,y), (z,w) at table columns j, j+1, bit-exact.
+__device__ __forceinline__ float4 rope4_exact(float4 x, const float* c, const float* s) {
+    const float2 a = rope_pair_exact(make_float2(x.x, x.y), c[0], s[0]);
+    const float2 b = rope_pair_exact(make_float2(x.z, x.w), c[1], s[1]);
+    return make_float4(a.x, a.y, b.x, b.y);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_amdgcn_update_dpp(0.0f, x, CTRL, 0xF, 0xF, false);
+}
+
+// Sum over aligned groups of LPG lanes; every lane of a group gets the total.
+template <int LPG>
+__device__ __forceinline__ float group_sum(float x) {
+    if constexpr (LPG >= 2) x += dpp<0xB1>(x);    // quad_perm [1,0,3,2]
+    if constexpr (LPG >= 4) x += dpp<0x4E>(x);    // quad_perm [2,3,0,1]
+    if constexpr (LPG >= 8) x += dpp<0x141>(x);   // row_half_mirror
+    if constexpr (LPG >= 16) x += dpp<0x140>(x);  // row_mirror
+    if constexpr (LPG >= 32) x += __shfl_xor(x, 16);
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+// Lanes per position group for each compiled head_dim: every lane holds
+// head_dim / LPG floats (a multiple of 4, for 128-bit loads).
+template <int HD>
+struct LaneCfg;
+template <> struct LaneCfg<16> { static constexpr int LPG = 4; };
+template <> struct LaneCfg<32> { static constexpr int LPG = 8; };
+template <> struct LaneCfg<48> { static constexpr int LPG = 4; };
+template <> struct LaneCfg<64> { static constexpr int LPG = 8; };
+template <> struct LaneCfg<96> { static constexpr int LPG = 8; };
+template <> struct LaneCfg<128> { static constexpr int LPG = 8; };
+template <> struct LaneCfg<256> { static constexpr int LPG = 16; };
+
+// One online-softmax step of a lane group over TP positions (log2 domain):
+// scores q.k for GB heads reduced over the LPG lanes of the group, running
+// max m, running sum l, accumulator o rescaled by 2^(m_old - m_new).
+// Positions with valid[tp] false contribute nothing.
+template <int LPG, int NV, int GB, int TP>
+__device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
+                                            const float4 (&kr)[TP][NV],
+                                            const float4 (&vr)[TP][NV], const bool (&valid)[TP],
+                                            float (&m)[GB], float (&l)[GB],
+                                            float4 (&o)[GB][NV]) {
+#pragma unroll
+    for (int i = 0; i < GB; ++i) {
+        float sc[TP];
+#pragma unroll
+        for (int tp = 0; tp < TP; ++tp) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                acc = fmaf(qr[i][v].x, kr[tp][v].x, acc);
+                acc = fmaf(qr[i][v].y, kr[tp][v].y, acc);
+                acc = fmaf(qr[i][v].z, kr[tp][v].z, acc);
+                acc = fmaf(qr[i][v].w, kr[tp][v].w, acc);
+            }
+            acc = group_sum<LPG>(acc);
+            sc[tp] = valid[tp] ? acc : -INFINITY;
+        }
+        float mx = sc[0];
+#pragma unroll
+        for (int tp = 1; tp < TP; ++tp) mx = fmaxf(mx, sc[tp]);
+        const float mn = fmaxf(m[i], mx);
+        const float mu = (mn == -INFINITY) ? 0.0f : mn;
+        const float alpha = fast_exp2(m[i] - mu);
+        float pr[TP];
+        float ps = 0.0f;
+#pragma unroll
+        for (int tp = 0; tp < TP; ++tp) {
+            pr[tp] = fast_exp2(sc[tp] - mu);
+            ps += pr[tp];
+        }
+        l[i] = l[i] * alpha + ps;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            float4 acc = o[i][v];
+            acc.x *= alpha;
+            acc.y *= alpha;
+            acc.z *= alpha;
+            acc.w *= alpha;
+#pragma unroll
+            for (int tp = 0; tp < TP; ++tp) {
+                acc.x = fmaf(pr[tp], vr[tp][v].x, acc.x);
+                acc.y = fmaf(pr[tp], vr[tp][v].y, acc.y);
+                acc.z = fmaf(pr[tp], vr[tp][v].z, acc.z);
+                acc.w = fmaf(pr[tp], vr[tp][v].w, acc.w);
+            }
+            o[i][v] = acc;
+        }
+        m[i] = mn;
+    }
+}
+
+// Merges the online-softmax states of the lane groups of a wave (lanes with
+// equal index inside their group hold equal head dims); afterwards every
+// lane holds the wave's state for its dims.
+template <int LPG, int NV, int GB>
+__device__ __forceinline__ void merge_lane_groups(float (&m)[GB], float (&l)[GB],
+                                                  float4 (&o)[GB][NV]) {
+#pragma unroll
+    for (int off = LPG; off < 64; off <<= 1) {
+#pragma unroll
+        for (int i = 0; i < GB; ++i) {
+            const float mo = __shfl_xor(m[i], off);
+            const float lo = __shfl_xor(l[i], off);
+            const float mn = fmaxf(m[i], mo);
+            const float mu = (mn == -INFINITY) ? 0.0f : mn;
+            const float wa = fast_exp2(m[i] - mu);
+            const float wb = fast_exp2(mo - mu);
+            l[i] = l[i] * wa + lo * wb;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float4 x = o[i][v];
+                x.x = x.x * wa + __shfl_xor(x.x, off) * wb;
+                x.y = x.y * wa + __shfl_xor(x.y, off) * wb;
+                x.z = x.z * wa + __shfl_xor(x.z, off) * wb;
+                x.w = x.w * wa + __shfl_xor(x.w, off) * wb;
+                o[i][v] = x;
+            }
+            m[i] = mn;
+        }
+    }
+}
+
+// Query heads that share one loaded K/V segment in a workgroup.
+inline int pick_gb(int kv_mul) {
+    for (int gb = 4; gb > 1; --gb)
+        if (kv_mul % gb == 0) return gb;
+    return 1;
+}
+
+}  // namespace slm

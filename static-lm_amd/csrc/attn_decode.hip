@@ -1,0 +1,389 @@
+// Single-token decode for gfx950: KV append fused into split-K attention,
+// then a log-sum-exp merge of the splits.
+//
+// Replaces, for one layer and position p, the decode attention block of
+// forward_token_with_kv (transformer.rs:413-443):
+//   K[p] = rope(k), V[p] = v                    (transformer.rs:416-428)
+//   out_h = sum_t softmax_t(q_h . K[t, g] / sqrt(hd)) V[t, g], t = 0..p,
+//   g = h / kv_mul                              (transformer.rs:273-321)
+//
+// Mapping.  blockIdx.x = split * groups + group, so workgroups that run at
+// the same time cover every KV head of the same positions (whole 4 KiB cache
+// rows for the Llama-3-8B shape).  A workgroup owns positions
+// [split*chunk, min(p+1, (split+1)*chunk)) of one KV head and GB of its
+// kv_mul query heads: each K/V segment loaded from HBM serves GB heads (the
+// reference re-reads it once per head).  In a wave, LPG lanes hold one
+// position's head_dim floats (128-bit nontemporal loads, LPG*16 contiguous
+// bytes per group); each lane group keeps its own online-softmax state
+// (log2 domain) over the positions it sees.  States merge across lane groups
+// with shuffles and across waves through LDS; a sequence that fits one split
+// is written out directly, otherwise decode_combine_kernel merges the split
+// partials.  (Merging in the last workgroup to finish needs device-scope
+// fences, which on this part write back and invalidate the whole L2: a
+// second small kernel is cheaper.)
+//
+// The workgroup owning position p does not read row p back: it rotates k in
+// registers with the reference's f32 arithmetic (no FMA contraction), stores
+// K[p] and V[p] (bit-exact with the reference), and seeds its state with
+// them.  No other workgroup reads row p.
+#include <math.h>
+
+#include "attn_common.h"
+#include "slm_internal.h"
+
+namespace slm {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxSplits = 1024;
+
+template <int HD, int GB>
+constexpr int dec_tp() {
+    constexpr int fpl = HD / LaneCfg<HD>::LPG;
+    return (fpl <= 8) ? 4 : ((GB <= 2) ? 4 : 2);
+}
+
+template <int HD, int GB>
+constexpr int dec_span() {
+    return kWaves * (64 / LaneCfg<HD>::LPG) * dec_tp<HD, GB>();
+}
+
+struct DecodeParams {
+    const float* q;      // [dim]; rotated at p here when cos_t != nullptr
+    const float* k_new;  // [kv_dim] appended at p when not nullptr
+    const float* v_new;
+    float* k_cache;      // layer K slice [max_seq_len][kv_dim]
+    float* v_cache;
+    const float* cos_t;  // RoPE tables [max_seq_len][head_dim/2]
+    const float* sin_t;
+    float* out;          // [dim]
+    float* part_o;       // [n_splits][num_heads][head_dim]
+    float* part_ml;      // [n_splits][num_heads][2]
+    int pos;
+    int chunk;
+    int n_splits;
+    int num_heads;
+    int kv_dim;
+    int kv_mul;
+    int half;
+    float scale_log2;
+};
+
+template <int HD, int GB>
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
+    constexpr int LPG = LaneCfg<HD>::LPG;
+    constexpr int FPL = HD / LPG;
+    constexpr int NV = FPL / 4;
+    constexpr int GPW = 64 / LPG;
+    constexpr int TP = dec_tp<HD, GB>();
+    constexpr int IT = kWaves * GPW * TP;
+    static_assert(FPL % 4 == 0, "lane slice must be whole float4s");
+
+    const int nhb = p.kv_mul / GB;
+    const int groups = (p.num_heads / p.kv_mul) * nhb;
+    const int split = blockIdx.x / groups;
+    const int gy = blockIdx.x - split * groups;
+    const int g = gy / nhb;
+    const int h0 = g * p.kv_mul + (gy % nhb) * GB;
+    const int seq_len = p.pos + 1;
+    const int t0 = split * p.chunk;
+    const int t1 = min(seq_len, t0 + p.chunk);
+    const bool append = p.k_new != nullptr;
+    const bool owner = t1 == seq_len;
+    const int t_end = (append && owner) ? p.pos : t1;  // rows read from the cache
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int li = lane % LPG;
+    const int lg = lane / LPG;
+    const long trow = (long)p.pos * p.half;
+    const float* kbase = p.k_cache + g * HD + 4 * li;
+    const float* vbase = p.v_cache + g * HD + 4 * li;
+
+    float4 kr[TP][NV], vr[TP][NV];
+    bool valid[TP];
+    auto load_tile = [&](int tb) {
+#pragma unroll
+        for (int tp = 0; tp < TP; ++tp) {
+            const int t = tb + (tp * kWaves + wave) * GPW + lg;
+            valid[tp] = t < t_end;
+            const long tt = valid[tp] ? t : t0;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                kr[tp][v] = ld4_stream(kbase + tt * p.kv_dim + 4 * v * LPG);
+                vr[tp][v] = ld4_stream(vbase + tt * p.kv_dim + 4 * v * LPG);
+            }
+        }
+    };
+    // the first tile's loads go out before the q set-up so they overlap it
+    if (t0 < t_end) load_tile(t0);
+
+    // q slice of each head: dims 4*(v*LPG + li) .. +3, rotated and pre-scaled
+    float4 qr[GB][NV];
+#pragma unroll
+    for (int i = 0; i < GB; ++i) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int d = 4 * (v * LPG + li);
+            float4 x = ld4(p.q + (h0 + i) * HD + d);
+            if (p.cos_t != nullptr)
+                x = rope4_exact(x, p.cos_t + trow + (d >> 1), p.sin_t + trow + (d >> 1));
+            x.x *= p.scale_log2;
+            x.y *= p.scale_log2;
+            x.z *= p.scale_log2;
+            x.w *= p.scale_log2;
+            qr[i][v] = x;
+        }
+    }
+
+    float m[GB], l[GB];
+    float4 o[GB][NV];
+#pragma unroll
+    for (int i = 0; i < GB; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) o[i][v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    if (append && owner) {
+        // the appended row, from registers
+        float4 kn[NV], vn[NV];
+        const bool writer = (gy % nhb) == 0 && wave == 0 && lg == 0;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int d = 4 * (v * LPG + li);
+            kn[v] = rope4_exact(ld4(p.k_new + g * HD + d), p.cos_t + trow + (d >> 1),
+                                p.sin_t + trow + (d >> 1));
+            vn[v] = ld4(p.v_new + g * HD + d);
+            if (writer) {
+                *reinterpret_cast<float4*>(p.k_cache + (long)p.pos * p.kv_dim + g * HD + d) = kn[v];
+                *reinterpret_cast<float4*>(p.v_cache + (long)p.pos * p.kv_dim + g * HD + d) = vn[v];
+            }
+        }
+        const bool seed = wave == 0 && lg == 0;
+#pragma unroll
+        for (int i = 0; i < GB; ++i) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                acc = fmaf(qr[i][v].x, kn[v].x, acc);
+                acc = fmaf(qr[i][v].y, kn[v].y, acc);
+                acc = fmaf(qr[i][v].z, kn[v].z, acc);
+                acc = fmaf(qr[i][v].w, kn[v].w, acc);
+            }
+            acc = group_sum<LPG>(acc);
+            if (seed) {
+                m[i] = acc;
+                l[i] = 1.0f;
+#pragma unroll
+                for (int v = 0; v < NV; ++v) o[i][v] = vn[v];
+            }
+        }
+    }
+
+    for (int tb = t0; tb < t_end; tb += IT) {
+        if (tb != t0) load_tile(tb);
+        attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
+    }
+    merge_lane_groups<LPG, NV, GB>(m, l, o);
+
+    // merge the waves through LDS: this split's (max, sum, acc) per head
+    __shared__ __align__(16) float s_o[kWaves][GB][HD];
+    __shared__ float s_m[kWaves][GB];
+    __shared__ float s_l[kWaves][GB];
+    if (lg == 0) {
+#pragma unroll
+        for (int i = 0; i < GB; ++i) {
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+                *reinterpret_cast<float4*>(&s_o[wave][i][4 * (v * LPG + li)]) = o[i][v];
+            if (li == 0) {
+                s_m[wave][i] = m[i];
+                s_l[wave][i] = l[i];
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < GB * HD; idx += kThreads) {
+        const int i = idx / HD;
+        const int d = idx - i * HD;
+        float mx = s_m[0][i];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][i]);
+        const float mu = (mx == -INFINITY) ? 0.0f : mx;
+        float acc_o = 0.0f, acc_l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float wt = fast_exp2(s_m[w][i] - mu);
+            acc_o += wt * s_o[w][i][d];
+            acc_l += wt * s_l[w][i];
+        }
+        const int h = h0 + i;
+        if (p.n_splits == 1) {
+            p.out[h * HD + d] = acc_o / acc_l;
+        } else {
+            const long pi = (long)split * p.num_heads + h;
+            p.part_o[pi * HD + d] = acc_o;
+            if (d == 0) {
+                p.part_ml[pi * 2] = mx;
+                p.part_ml[pi * 2 + 1] = acc_l;
+            }
+        }
+    }
+}
+
+// Log-sum-exp merge of the split partials: one workgroup per (head, 64 head
+// dims).  Every load of a phase is issued before any is used, so each phase
+// costs one memory latency.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p) {
+    constexpr int DW = HD < 64 ? HD : 64;  // head dims per workgroup
+    __shared__ float s_w[kMaxSplits];
+    __shared__ float s_acc[kWaves][DW];
+    __shared__ float s_ltot;
+    const int h = blockIdx.x;
+    const int d = blockIdx.y * DW + (threadIdx.x & 63);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int ns = p.n_splits;
+    const float2* ml = reinterpret_cast<const float2*>(p.part_ml);
+    if (wave == 0) {
+        constexpr int R = kMaxSplits / 64;
+        float2 v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int sp = lane + 64 * r;
+            v[r] = sp < ns ? ml[(long)sp * p.num_heads + h] : make_float2(-INFINITY, 0.0f);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < R; ++r) mx = fmaxf(mx, v[r].x);
+        mx = wave_max(mx);
+        float ls = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int sp = lane + 64 * r;
+            if (sp < ns) {
+                const float w = fast_exp2(v[r].x - mx);
+                s_w[sp] = w;
+                ls += w * v[r].y;
+            }
+        }
+        ls = wave_sum(ls);
+        if (lane == 0) s_ltot = ls;
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    if (lane < DW) {
+        const float* src = p.part_o + (long)h * HD + d;
+        const long stride = (long)p.num_heads * HD;
+        int sp = wave;
+        for (; sp + 7 * kWaves < ns; sp += 8 * kWaves) {
+            float x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = src[(long)(sp + u * kWaves) * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += s_w[sp + u * kWaves] * x[u];
+        }
+        for (; sp < ns; sp += kWaves) acc += s_w[sp] * src[(long)sp * stride];
+        s_acc[wave][lane] = acc;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < DW) {
+        const float tot = s_acc[0][lane] + s_acc[1][lane] + s_acc[2][lane] + s_acc[3][lane];
+        p.out[h * HD + d] = tot / s_ltot;
+    }
+}
+
+template <int HD, int GB>
+hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st) {
+    const int groups = s.num_kv_heads * (s.kv_mul / GB);
+    hipLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups), dim3(kThreads),
+                       0, st, dp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || dp.n_splits == 1) return e;
+    constexpr int DW = HD < 64 ? HD : 64;
+    hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads, HD / DW), dim3(kThreads), 0,
+                       st, dp);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_hd(const Shape& s, const DecodeParams& dp, hipStream_t st) {
+    switch (pick_gb(s.kv_mul)) {
+        case 4: return launch_t<HD, 4>(s, dp, st);
+        case 3: return launch_t<HD, 3>(s, dp, st);
+        case 2: return launch_t<HD, 2>(s, dp, st);
+        default: return launch_t<HD, 1>(s, dp, st);
+    }
+}
+
+template <int HD>
+int span_hd(int kv_mul) {
+    switch (pick_gb(kv_mul)) {
+        case 4: return dec_span<HD, 4>();
+        case 3: return dec_span<HD, 3>();
+        case 2: return dec_span<HD, 2>();
+        default: return dec_span<HD, 1>();
+    }
+}
+
+int decode_span(const Shape& s) {
+    switch (s.head_dim) {
+        case 16: return span_hd<16>(s.kv_mul);
+        case 32: return span_hd<32>(s.kv_mul);
+        case 48: return span_hd<48>(s.kv_mul);
+        case 64: return span_hd<64>(s.kv_mul);
+        case 96: return span_hd<96>(s.kv_mul);
+        case 128: return span_hd<128>(s.kv_mul);
+        case 256: return span_hd<256>(s.kv_mul);
+        default: return 64;
+    }
+}
+
+}  // namespace
+
+int decode_groups(const Shape& s) { return s.num_kv_heads * (s.kv_mul / pick_gb(s.kv_mul)); }
+
+int decode_max_splits() { return kMaxSplits; }
+
+void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* chunk) {
+    // About 4 workgroups per CU on long sequences, each walking at least 8
+    // loop iterations, at most kMaxSplits splits.  A pure function of seq_len
+    // and the shape, so results reproduce run to run.
+    const int it = decode_span(s);
+    const int groups = decode_groups(s);
+    const int want = groups >= 1024 ? 1 : 1024 / groups;
+    int c = (seq_len + want - 1) / want;
+    if (c < 8 * it) c = 8 * it;
+    c = (c + it - 1) / it * it;
+    if ((seq_len + c - 1) / c > kMaxSplits) {
+        c = (seq_len + kMaxSplits - 1) / kMaxSplits;
+        c = (c + it - 1) / it * it;
+    }
+    *chunk = c;
+    *n_splits = (seq_len + c - 1) / c;
+}
+
+hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st) {
+    DecodeParams dp{a.q,        a.k_new,   a.v_new,     a.k_cache,  a.v_cache,
+                    a.cos_t,    a.sin_t,   a.out,       a.part_o,   a.part_ml,
+                    a.pos,      a.chunk,   a.n_splits,  s.num_heads,
+                    s.kv_dim,   s.kv_mul,  s.half,
+                    1.4426950408889634f / sqrtf((float)s.head_dim)};
+    if (a.n_splits < 1 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
+    switch (s.head_dim) {
+        case 16: return launch_hd<16>(s, dp, st);
+        case 32: return launch_hd<32>(s, dp, st);
+        case 48: return launch_hd<48>(s, dp, st);
+        case 64: return launch_hd<64>(s, dp, st);
+        case 96: return launch_hd<96>(s, dp, st);
+        case 128: return launch_hd<128>(s, dp, st);
+        case 256: return launch_hd<256>(s, dp, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace slm

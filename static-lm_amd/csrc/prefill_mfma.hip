@@ -27,6 +27,7 @@
 // running sum stays a per-lane partial until the end.
 #include <math.h>
 
+#include "attn_common.h"
 #include "slm_internal.h"
 
 namespace slm {
@@ -38,10 +39,6 @@ constexpr int kKT = 32;  // keys per LDS tile
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ float4 ld4(const float* p) {
-    return *reinterpret_cast<const float4*>(p);
 }
 
 struct PrefillParams {
@@ -114,13 +111,7 @@ prefill_mfma_kernel(PrefillParams p) {
 #pragma unroll
         for (int c = 0; c < DPL / 4; ++c) {
             float4 x = ok ? ld4(src + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (p.cos_t != nullptr) {
-                const float c0 = p.cos_t[tr + 2 * c], s0 = p.sin_t[tr + 2 * c];
-                const float c1 = p.cos_t[tr + 2 * c + 1], s1 = p.sin_t[tr + 2 * c + 1];
-                const float x0 = x.x * c0 - x.y * s0, x1 = x.x * s0 + x.y * c0;
-                const float x2 = x.z * c1 - x.w * s1, x3 = x.z * s1 + x.w * c1;
-                x = make_float4(x0, x1, x2, x3);
-            }
+            if (p.cos_t != nullptr) x = rope4_exact(x, p.cos_t + tr + 2 * c, p.sin_t + tr + 2 * c);
             qf[qt][4 * c + 0] = x.x * p.scale_log2;
             qf[qt][4 * c + 1] = x.y * p.scale_log2;
             qf[qt][4 * c + 2] = x.z * p.scale_log2;

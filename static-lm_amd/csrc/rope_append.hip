@@ -6,22 +6,11 @@
 // with each product and each sum rounded on its own (Rust never fuses), so the
 // cache rows written here are bit-identical to the reference's.  Contraction
 // into v_fma is switched off in these kernels for that reason.
+#include "attn_common.h"
 #include "slm_internal.h"
 
 namespace slm {
 namespace {
-
-__device__ __forceinline__ float2 rotate_pair(float2 x, float c, float s) {
-#pragma clang fp contract(off)
-    const float t0 = x.x * c;
-    const float t1 = x.y * s;
-    const float t2 = x.x * s;
-    const float t3 = x.y * c;
-    float2 r;
-    r.x = t0 - t1;
-    r.y = t2 + t3;
-    return r;
-}
 
 // One thread per (row, pair).  K row pos0+r of the layer slice receives the
 // rotated pair, V row receives the v pair unchanged (the Wk/Wv GEMV output the
@@ -42,7 +31,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     const float s = sin_t[pos * half + j];
     const float2 kk = reinterpret_cast<const float2*>(k + (long)r * kv_dim)[p];
     const float2 vv = reinterpret_cast<const float2*>(v + (long)r * kv_dim)[p];
-    reinterpret_cast<float2*>(k_cache + pos * kv_dim)[p] = rotate_pair(kk, c, s);
+    reinterpret_cast<float2*>(k_cache + pos * kv_dim)[p] = rope_pair_exact(kk, c, s);
     reinterpret_cast<float2*>(v_cache + pos * kv_dim)[p] = vv;
 }
 
@@ -57,7 +46,7 @@ __global__ __launch_bounds__(256) void rope_kernel(
     const unsigned j = p % (unsigned)half;
     const long pos = pos0 + (long)r;
     float2* row = reinterpret_cast<float2*>(x + (long)r * row_len);
-    row[p] = rotate_pair(row[p], cos_t[pos * half + j], sin_t[pos * half + j]);
+    row[p] = rope_pair_exact(row[p], cos_t[pos * half + j], sin_t[pos * half + j]);
 }
 
 }  // namespace

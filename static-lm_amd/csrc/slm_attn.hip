@@ -250,69 +250,56 @@ int do_append(slm_attn_ctx* c, int layer, int pos0, int n, const float* k,
     return launch_status(c, e, "kv_append kernel launch");
 }
 
+// Single-token decode at pos: with k_new/v_new the KV row is appended and q
+// is rotated at pos inside the kernel; without them q is already rotated and
+// row pos is read from the cache.
+int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* k_new,
+              const float* v_new, float* out, bool rotate) {
+    const slm::Shape& s = c->shape;
+    int ns = 1, chunk = 1;
+    slm::decode_split_policy(s, pos + 1, &ns, &chunk);
+    slm::DecodeArgs a{q,
+                      k_new,
+                      v_new,
+                      k_base(c, layer),
+                      v_base(c, layer),
+                      rotate ? c->cos_t : nullptr,
+                      rotate ? c->sin_t : nullptr,
+                      out,
+                      c->part_o,
+                      c->part_ml,
+                      pos,
+                      chunk,
+                      ns};
+    Timed t(c, SLM_K_DECODE);
+    hipError_t e = slm::launch_decode(s, a, c->stream);
+    t.done();
+    return launch_status(c, e, "decode kernel launch");
+}
+
 // Attention of rows b < n at positions start + b over cache rows 0..start+b.
 // rotate: q is un-rotated and the kernels apply RoPE at each row's position.
 int do_attend(slm_attn_ctx* c, int layer, int start, int n, const float* q,
               float* out, bool rotate) {
     const slm::Shape& s = c->shape;
-    if (n > 1 && slm::prefill_mfma_supported(s)) {
+    if (n == 1) return do_decode(c, layer, start, q, nullptr, nullptr, out, rotate);
+    Timed t(c, SLM_K_PREFILL);
+    hipError_t e;
+    if (slm::prefill_mfma_supported(s)) {
         slm::PrefillArgs pa{q,          k_base(c, layer), v_base(c, layer),
                             rotate ? c->cos_t : nullptr,
                             rotate ? c->sin_t : nullptr, out, start, n};
-        Timed t(c, SLM_K_PREFILL);
-        hipError_t e = slm::launch_prefill_mfma(s, pa, c->stream);
-        t.done();
-        return launch_status(c, e, "prefill kernel launch");
-    }
-    if (n == 1) {
-        int ns = 1, chunk = 1;
-        slm::decode_split_policy(s, start + 1, &ns, &chunk);
-        slm::RowsArgs a{q,      k_base(c, layer),
+        e = slm::launch_prefill_mfma(s, pa, c->stream);
+    } else {
+        slm::RowsArgs a{q,   k_base(c, layer),
                         v_base(c, layer),
                         rotate ? c->cos_t : nullptr,
                         rotate ? c->sin_t : nullptr,
-                        out,    c->part_o,
-                        c->part_ml,
-                        start,  1,
-                        chunk,  ns};
-        {
-            Timed t(c, SLM_K_DECODE_SPLIT);
-            hipError_t e = slm::launch_attn_rows(s, a, c->stream);
-            t.done();
-            if (e != hipSuccess) return hip_fail(c, e, "decode kernel launch");
-        }
-        if (ns > 1) {
-            Timed t(c, SLM_K_DECODE_COMBINE);
-            hipError_t e = slm::launch_attn_combine(s, a, c->stream);
-            t.done();
-            if (e != hipSuccess)
-                return hip_fail(c, e, "decode combine kernel launch");
-        }
-        return SLM_OK;
+                        out, start, n};
+        e = slm::launch_attn_rows(s, a, c->stream);
     }
-    // Rows kernel with one split per row: each workgroup walks its row's
-    // whole causal range and writes the normalised output.
-    const int kMaxRows = 65535;
-    for (int b0 = 0; b0 < n; b0 += kMaxRows) {
-        const int nb = (n - b0 < kMaxRows) ? n - b0 : kMaxRows;
-        slm::RowsArgs a{q + (size_t)b0 * s.dim,
-                        k_base(c, layer),
-                        v_base(c, layer),
-                        rotate ? c->cos_t : nullptr,
-                        rotate ? c->sin_t : nullptr,
-                        out + (size_t)b0 * s.dim,
-                        nullptr,
-                        nullptr,
-                        start + b0,
-                        nb,
-                        c->cfg.max_seq_len,
-                        1};
-        Timed t(c, SLM_K_PREFILL);
-        hipError_t e = slm::launch_attn_rows(s, a, c->stream);
-        t.done();
-        if (e != hipSuccess) return hip_fail(c, e, "prefill kernel launch");
-    }
-    return SLM_OK;
+    t.done();
+    return launch_status(c, e, "prefill kernel launch");
 }
 
 int ensure_stage(slm_attn_ctx* c, size_t floats) {
@@ -417,7 +404,7 @@ int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
     if (e == hipSuccess)
         e = hipMalloc(&c->part_ml,
                       (size_t)max_splits * s.num_heads * 2 * sizeof(float));
-    if (e != hipSuccess) return bail(hip_fail(nullptr, e, "hipMalloc(partials)"));
+    if (e != hipSuccess) return bail(hip_fail(nullptr, e, "hipMalloc(decode partials)"));
 
     *out = c;
     return SLM_OK;
@@ -521,8 +508,7 @@ int slm_attn_decode_dev(slm_attn_ctx* c, int32_t layer, int32_t pos,
                               {{q, s.dim}, {k, s.kv_dim}, {v, s.kv_dim}},
                               true)))
         return rc;
-    if ((rc = do_append(c, layer, pos, 1, k, v))) return rc;
-    return do_attend(c, layer, pos, 1, q, out, true);
+    return do_decode(c, layer, pos, q, k, v, out, true);
 }
 
 int slm_attn_prefill_dev(slm_attn_ctx* c, int32_t layer, int32_t start,

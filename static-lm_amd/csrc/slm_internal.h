@@ -30,32 +30,43 @@ hipError_t launch_kv_append(const Shape& s, const float* k, const float* v,
 hipError_t launch_rope(const Shape& s, float* x, int n, int row_len, int pos0,
                        const float* cos_t, const float* sin_t, hipStream_t st);
 
-// Split-K attention over cache rows, one query row per blockIdx.z.
+// Batched attention rows, one workgroup per (row, KV head x head batch)
+// walking the row's whole causal range (no split).
 struct RowsArgs {
-    const float* q;      // [rows][dim], head h at h*head_dim
+    const float* q;        // [rows][dim], head h at h*head_dim
     const float* k_cache;  // layer K base, [max_seq_len][kv_dim]
     const float* v_cache;  // layer V base
-    const float* cos_t;  // RoPE tables, or nullptr when q is already rotated
+    const float* cos_t;    // RoPE tables, or nullptr when q is already rotated
     const float* sin_t;
-    float* out;          // [rows][dim], written when a row has one split
-    float* part_o;       // [rows][max_splits][num_heads][head_dim]
-    float* part_ml;      // [rows][max_splits][num_heads][2] (max, sum)
-    int start;           // row r sits at position start + r
+    float* out;            // [rows][dim]
+    int start;             // row r sits at position start + r
     int rows;
-    int chunk;           // positions per split
-    int max_splits;      // grid.x
 };
-
-// Chooses the decode split: n_splits and chunk as a pure function of
-// seq_len and the shape.  Also the positions one workgroup iteration covers.
-void decode_split_policy(const Shape& s, int seq_len, int* n_splits,
-                         int* chunk);
-int rows_iteration_span(const Shape& s);
+hipError_t launch_attn_rows(const Shape& s, const RowsArgs& a, hipStream_t st);
 bool head_dim_supported(int head_dim);
 
-hipError_t launch_attn_rows(const Shape& s, const RowsArgs& a, hipStream_t st);
-hipError_t launch_attn_combine(const Shape& s, const RowsArgs& a,
-                               hipStream_t st);
+// Single-token decode: optional KV append at pos fused into split-K
+// attention over rows 0..pos, then a merge kernel when there are splits.
+struct DecodeArgs {
+    const float* q;      // [dim]; rotated at pos when cos_t != nullptr
+    const float* k_new;  // [kv_dim] appended at pos when not nullptr
+    const float* v_new;
+    float* k_cache;
+    float* v_cache;
+    const float* cos_t;
+    const float* sin_t;
+    float* out;          // [dim]
+    float* part_o;       // [n_splits][num_heads][head_dim]
+    float* part_ml;      // [n_splits][num_heads][2]
+    int pos;
+    int chunk;
+    int n_splits;
+};
+// n_splits and chunk as a pure function of seq_len and the shape.
+void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* chunk);
+int decode_groups(const Shape& s);
+int decode_max_splits();
+hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st);
 
 // Causal prefill on fp32 MFMA: rows b < n at positions start + b attend to
 // cache rows 0..start+b.  q is un-rotated when cos_t != nullptr.
