@@ -62,6 +62,22 @@ def prefill_flops(start: int, n: int) -> int:
     return 4 * HD * HEADS * s
 
 
+TRAFFIC_PROFILE = REPO / "profiles" / "decode_kernel_llama3-8b_ctx32k_ctx131k.md"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the 32k decode kernel from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy calibration),
+    or None when the summary is absent."""
+    try:
+        for ln in TRAFFIC_PROFILE.read_text().splitlines():
+            if ln.startswith("traffic_bytes_per_launch(decode_kernel @ pos 32767):"):
+                return int(ln.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def host_cpu() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -277,6 +293,9 @@ def main() -> int:
                     help="time budget of the CPU baseline sample (0 skips it)")
     ap.add_argument("--skip-extra", action="store_true",
                     help="only the headline decode @32k measurement")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run one device-to-device copy of this many MiB: a plain "
+                         "copy kernel of known size that scales rocprofv3 byte counters")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -297,6 +316,17 @@ def main() -> int:
     # C ABI reads as "the context's own stream".  Every kernel of the library
     # and every timing event goes on this one stream.
     torch.cuda.set_stream(torch.cuda.Stream())
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 18  # floats
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty(n, device="cuda")
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {args.copy_calibration_mib} MiB read + "
+            f"{args.copy_calibration_mib} MiB written")
+        del src, dst
 
     log("decode @32k")
     d = bench_decode_32k(torch, P, args.steps, args.warmup)
@@ -351,12 +381,14 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_rows_kernel<128,4> (split-K decode)",
+            "kernel": "decode_kernel<128,4> (append + split-K decode)",
             "achieved": round(d["split_kernel_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(d["split_kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
+                              + TRAFFIC_PROFILE.name,
             "avg_launch_us": round(d["split_kernel_avg_us"], 3),
             "algorithmic_bytes_per_launch": d["split_kernel_bytes"],
         },

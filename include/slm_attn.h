@@ -47,7 +47,7 @@ extern "C" {
 #define SLM_ERR_POS (-2)
 /* n == 0 or start + n > max_seq_len (transformer.rs:501-502). */
 #define SLM_ERR_BATCH (-3)
-/* layer index outside 0..num_layers (the layer-count assert, transformer.rs:777-781). */
+/* layer index outside 0..num_layers (the layer-count assert, transformer.rs:761-766). */
 #define SLM_ERR_LAYER (-4)
 /* out overlaps q, k, v or the KV region (attention_slices, arena.rs:272-280). */
 #define SLM_ERR_ALIAS (-5)
