@@ -145,6 +145,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
     prof = ctx.profile_read()
     ctx.profile(False)
     n_split, split_ms = prof["decode"]
+    n_comb, comb_ms = prof["combine"]
     avg_split_s = split_ms / max(n_split, 1) / 1e3
     kv_bytes = 2 * (pos + 1) * KV_DIM * 4
     achieved = kv_bytes / avg_split_s / 1e9
@@ -158,6 +159,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
         "profile": prof, "split_kernel_avg_us": avg_split_s * 1e6,
         "split_kernel_bytes": kv_bytes, "split_kernel_gbs": achieved,
         "splits": ns, "chunk": chunk, "finite": finite,
+        "combine_avg_us": comb_ms / max(n_comb, 1) * 1e3,
     }
 
 
@@ -390,6 +392,7 @@ def main() -> int:
             "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
                               + TRAFFIC_PROFILE.name,
             "avg_launch_us": round(d["split_kernel_avg_us"], 3),
+            "combine_kernel_avg_us": round(d["combine_avg_us"], 3),
             "algorithmic_bytes_per_launch": d["split_kernel_bytes"],
         },
         "cpu_baseline": cpu,

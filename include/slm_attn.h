@@ -177,10 +177,11 @@ int slm_rope_tables_read(slm_attn_ctx* ctx, float* cos_out, float* sin_out);
  * Reading resets the counters. */
 enum {
     SLM_K_APPEND = 0,  /* rope(k) + KV append of a prefill batch */
-    SLM_K_DECODE = 1,  /* fused decode: append + split-K attention + merge */
-    SLM_K_PREFILL = 2, /* causal prefill attention */
-    SLM_K_ROPE = 3,    /* standalone rope */
-    SLM_K_COUNT = 4
+    SLM_K_DECODE = 1,  /* decode: in-kernel KV append + split-K attention */
+    SLM_K_COMBINE = 2, /* merge of the decode split partials */
+    SLM_K_PREFILL = 3, /* causal prefill attention */
+    SLM_K_ROPE = 4,    /* standalone rope */
+    SLM_K_COUNT = 5
 };
 typedef struct slm_kernel_stat {
     int64_t launches;

@@ -40,7 +40,7 @@ ERRORS = {
 ERR_CONFIG, ERR_POS, ERR_BATCH, ERR_LAYER, ERR_ALIAS, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_DEVICE = (
     -1, -2, -3, -4, -5, -6, -7, -8, -9)
 
-KERNEL_KINDS = ("append", "decode", "prefill", "rope")
+KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope")
 
 
 class SlmAttnError(RuntimeError):

@@ -38,15 +38,25 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxSplits = 1024;
 
-template <int HD, int GB>
-constexpr int dec_tp() {
-    constexpr int fpl = HD / LaneCfg<HD>::LPG;
-    return (fpl <= 8) ? 4 : ((GB <= 2) ? 4 : 2);
-}
+// Decode tiling per head_dim: lanes per position (LPG, 8 floats per lane
+// where head_dim allows) and positions per lane group per loop iteration
+// (TP).  Measured on MI355X for hd 128 at 32k and 131k context: 16 lanes x
+// 8 floats with one position per iteration keeps registers low enough
+// (~124 VGPRs) for several waves per SIMD and beat 8 lanes x 16 floats by
+// 5-7 points of HBM bandwidth.
+template <int HD>
+struct DecodeCfg;
+template <> struct DecodeCfg<16> { static constexpr int LPG = 2, TP = 2; };
+template <> struct DecodeCfg<32> { static constexpr int LPG = 4, TP = 2; };
+template <> struct DecodeCfg<48> { static constexpr int LPG = 4, TP = 2; };
+template <> struct DecodeCfg<64> { static constexpr int LPG = 8, TP = 2; };
+template <> struct DecodeCfg<96> { static constexpr int LPG = 8, TP = 2; };
+template <> struct DecodeCfg<128> { static constexpr int LPG = 16, TP = 1; };
+template <> struct DecodeCfg<256> { static constexpr int LPG = 32, TP = 1; };
 
-template <int HD, int GB>
+template <int HD>
 constexpr int dec_span() {
-    return kWaves * (64 / LaneCfg<HD>::LPG) * dec_tp<HD, GB>();
+    return kWaves * (64 / DecodeCfg<HD>::LPG) * DecodeCfg<HD>::TP;
 }
 
 struct DecodeParams {
@@ -70,14 +80,17 @@ struct DecodeParams {
     float scale_log2;
 };
 
-template <int HD, int GB>
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
-    constexpr int LPG = LaneCfg<HD>::LPG;
+// Tiling of decode_kernel: lanes per position (LPG), positions per lane group
+// per loop iteration (TP) and waves per workgroup (NW).
+template <int HD, int GB, int LPG_ = DecodeCfg<HD>::LPG, int TP_ = DecodeCfg<HD>::TP,
+          int NW = kWaves>
+__global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
+    constexpr int LPG = LPG_;
     constexpr int FPL = HD / LPG;
     constexpr int NV = FPL / 4;
     constexpr int GPW = 64 / LPG;
-    constexpr int TP = dec_tp<HD, GB>();
-    constexpr int IT = kWaves * GPW * TP;
+    constexpr int TP = TP_;
+    constexpr int IT = NW * GPW * TP;
     static_assert(FPL % 4 == 0, "lane slice must be whole float4s");
 
     const int nhb = p.kv_mul / GB;
@@ -106,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     auto load_tile = [&](int tb) {
 #pragma unroll
         for (int tp = 0; tp < TP; ++tp) {
-            const int t = tb + (tp * kWaves + wave) * GPW + lg;
+            const int t = tb + (tp * NW + wave) * GPW + lg;
             valid[tp] = t < t_end;
             const long tt = valid[tp] ? t : t0;
 #pragma unroll
@@ -190,9 +203,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     merge_lane_groups<LPG, NV, GB>(m, l, o);
 
     // merge the waves through LDS: this split's (max, sum, acc) per head
-    __shared__ __align__(16) float s_o[kWaves][GB][HD];
-    __shared__ float s_m[kWaves][GB];
-    __shared__ float s_l[kWaves][GB];
+    __shared__ __align__(16) float s_o[NW][GB][HD];
+    __shared__ float s_m[NW][GB];
+    __shared__ float s_l[NW][GB];
     if (lg == 0) {
 #pragma unroll
         for (int i = 0; i < GB; ++i) {
@@ -206,16 +219,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < GB * HD; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < GB * HD; idx += 64 * NW) {
         const int i = idx / HD;
         const int d = idx - i * HD;
         float mx = s_m[0][i];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][i]);
+        for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_m[w][i]);
         const float mu = (mx == -INFINITY) ? 0.0f : mx;
         float acc_o = 0.0f, acc_l = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float wt = fast_exp2(s_m[w][i] - mu);
             acc_o += wt * s_o[w][i][d];
             acc_l += wt * s_l[w][i];
@@ -235,11 +248,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
 }
 
 // Log-sum-exp merge of the split partials: one workgroup per (head, 64 head
-// dims).  Every load of a phase is issued before any is used, so each phase
-// costs one memory latency.
+// dims).  The partial accumulators of a round of up to 64 splits are loaded
+// before the split weights are known, so a round costs one memory latency.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p) {
     constexpr int DW = HD < 64 ? HD : 64;  // head dims per workgroup
+    constexpr int U = 16;                   // splits per wave per round
     __shared__ float s_w[kMaxSplits];
     __shared__ float s_acc[kWaves][DW];
     __shared__ float s_ltot;
@@ -248,8 +262,18 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int ns = p.n_splits;
-    const float2* ml = reinterpret_cast<const float2*>(p.part_ml);
+    const float* src = p.part_o + (long)h * HD + (lane < DW ? d : 0);
+    const long stride = (long)p.num_heads * HD;
+
+    // first round of accumulator loads, in flight while the weights are built
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int sp = wave + kWaves * u;
+        x[u] = sp < ns ? src[(long)sp * stride] : 0.0f;
+    }
     if (wave == 0) {
+        const float2* ml = reinterpret_cast<const float2*>(p.part_ml);
         constexpr int R = kMaxSplits / 64;
         float2 v[R];
 #pragma unroll
@@ -276,20 +300,21 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
     }
     __syncthreads();
     float acc = 0.0f;
-    if (lane < DW) {
-        const float* src = p.part_o + (long)h * HD + d;
-        const long stride = (long)p.num_heads * HD;
-        int sp = wave;
-        for (; sp + 7 * kWaves < ns; sp += 8 * kWaves) {
-            float x[8];
+    for (int base = 0; base < ns; base += kWaves * U) {
+        if (base > 0) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) x[u] = src[(long)(sp + u * kWaves) * stride];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc += s_w[sp + u * kWaves] * x[u];
+            for (int u = 0; u < U; ++u) {
+                const int sp = base + wave + kWaves * u;
+                x[u] = sp < ns ? src[(long)sp * stride] : 0.0f;
+            }
         }
-        for (; sp < ns; sp += kWaves) acc += s_w[sp] * src[(long)sp * stride];
-        s_acc[wave][lane] = acc;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int sp = base + wave + kWaves * u;
+            if (sp < ns) acc += s_w[sp] * x[u];
+        }
     }
+    if (lane < DW) s_acc[wave][lane] = acc;
     __syncthreads();
     if (wave == 0 && lane < DW) {
         const float tot = s_acc[0][lane] + s_acc[1][lane] + s_acc[2][lane] + s_acc[3][lane];
@@ -302,8 +327,11 @@ hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st) {
     const int groups = s.num_kv_heads * (s.kv_mul / GB);
     hipLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups), dim3(kThreads),
                        0, st, dp);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || dp.n_splits == 1) return e;
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_combine_t(const Shape& s, const DecodeParams& dp, hipStream_t st) {
     constexpr int DW = HD < 64 ? HD : 64;
     hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads, HD / DW), dim3(kThreads), 0,
                        st, dp);
@@ -320,25 +348,15 @@ hipError_t launch_hd(const Shape& s, const DecodeParams& dp, hipStream_t st) {
     }
 }
 
-template <int HD>
-int span_hd(int kv_mul) {
-    switch (pick_gb(kv_mul)) {
-        case 4: return dec_span<HD, 4>();
-        case 3: return dec_span<HD, 3>();
-        case 2: return dec_span<HD, 2>();
-        default: return dec_span<HD, 1>();
-    }
-}
-
 int decode_span(const Shape& s) {
     switch (s.head_dim) {
-        case 16: return span_hd<16>(s.kv_mul);
-        case 32: return span_hd<32>(s.kv_mul);
-        case 48: return span_hd<48>(s.kv_mul);
-        case 64: return span_hd<64>(s.kv_mul);
-        case 96: return span_hd<96>(s.kv_mul);
-        case 128: return span_hd<128>(s.kv_mul);
-        case 256: return span_hd<256>(s.kv_mul);
+        case 16: return dec_span<16>();
+        case 32: return dec_span<32>();
+        case 48: return dec_span<48>();
+        case 64: return dec_span<64>();
+        case 96: return dec_span<96>();
+        case 128: return dec_span<128>();
+        case 256: return dec_span<256>();
         default: return 64;
     }
 }
@@ -350,12 +368,12 @@ int decode_groups(const Shape& s) { return s.num_kv_heads * (s.kv_mul / pick_gb(
 int decode_max_splits() { return kMaxSplits; }
 
 void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* chunk) {
-    // About 4 workgroups per CU on long sequences, each walking at least 8
-    // loop iterations, at most kMaxSplits splits.  A pure function of seq_len
-    // and the shape, so results reproduce run to run.
+    // About 512 workgroups (two per CU) on long sequences, each walking at
+    // least 8 loop iterations, at most kMaxSplits splits.  A pure function of
+    // seq_len and the shape, so results reproduce run to run.
     const int it = decode_span(s);
     const int groups = decode_groups(s);
-    const int want = groups >= 1024 ? 1 : 1024 / groups;
+    const int want = groups >= 512 ? 1 : 512 / groups;
     int c = (seq_len + want - 1) / want;
     if (c < 8 * it) c = 8 * it;
     c = (c + it - 1) / it * it;
@@ -367,12 +385,31 @@ void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* chunk)
     *n_splits = (seq_len + c - 1) / c;
 }
 
-hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st) {
-    DecodeParams dp{a.q,        a.k_new,   a.v_new,     a.k_cache,  a.v_cache,
+static DecodeParams decode_params(const Shape& s, const DecodeArgs& a) {
+    return DecodeParams{a.q,        a.k_new,   a.v_new,     a.k_cache,  a.v_cache,
                     a.cos_t,    a.sin_t,   a.out,       a.part_o,   a.part_ml,
                     a.pos,      a.chunk,   a.n_splits,  s.num_heads,
                     s.kv_dim,   s.kv_mul,  s.half,
                     1.4426950408889634f / sqrtf((float)s.head_dim)};
+}
+
+hipError_t launch_decode_combine(const Shape& s, const DecodeArgs& a, hipStream_t st) {
+    const DecodeParams dp = decode_params(s, a);
+    if (a.n_splits < 2 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
+    switch (s.head_dim) {
+        case 16: return launch_combine_t<16>(s, dp, st);
+        case 32: return launch_combine_t<32>(s, dp, st);
+        case 48: return launch_combine_t<48>(s, dp, st);
+        case 64: return launch_combine_t<64>(s, dp, st);
+        case 96: return launch_combine_t<96>(s, dp, st);
+        case 128: return launch_combine_t<128>(s, dp, st);
+        case 256: return launch_combine_t<256>(s, dp, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st) {
+    const DecodeParams dp = decode_params(s, a);
     if (a.n_splits < 1 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
     switch (s.head_dim) {
         case 16: return launch_hd<16>(s, dp, st);

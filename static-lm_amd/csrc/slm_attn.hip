@@ -271,10 +271,17 @@ int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* 
                       pos,
                       chunk,
                       ns};
-    Timed t(c, SLM_K_DECODE);
-    hipError_t e = slm::launch_decode(s, a, c->stream);
+    {
+        Timed t(c, SLM_K_DECODE);
+        hipError_t e = slm::launch_decode(s, a, c->stream);
+        t.done();
+        if (e != hipSuccess) return hip_fail(c, e, "decode kernel launch");
+    }
+    if (ns == 1) return SLM_OK;
+    Timed t(c, SLM_K_COMBINE);
+    hipError_t e = slm::launch_decode_combine(s, a, c->stream);
     t.done();
-    return launch_status(c, e, "decode kernel launch");
+    return launch_status(c, e, "decode combine kernel launch");
 }
 
 // Attention of rows b < n at positions start + b over cache rows 0..start+b.

@@ -67,6 +67,8 @@ void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* chunk)
 int decode_groups(const Shape& s);
 int decode_max_splits();
 hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st);
+// Merge of the split partials; needed only when a.n_splits > 1.
+hipError_t launch_decode_combine(const Shape& s, const DecodeArgs& a, hipStream_t st);
 
 // Causal prefill on fp32 MFMA: rows b < n at positions start + b attend to
 // cache rows 0..start+b.  q is un-rotated when cos_t != nullptr.
