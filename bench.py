@@ -232,6 +232,63 @@ def bench_decode_131k(torch, P) -> dict:
             "gbs": total / (ms / 1e3) / 1e9}
 
 
+# The BASELINE.json configurations: (name, dim, heads, kv_heads, hd, layers, max_seq_len,
+# theta, prefill rows, decode steps, pre-filled rows)
+WORKLOADS = [
+    ("c1 synthetic dim256 4/4 hd64 2L msl512", 256, 4, 4, 2, 512, 1e4, 16, 8, 0),
+    ("c2 stories15m dim288 6/6 hd48 6L msl256", 288, 6, 6, 6, 256, 1e4, 16, 64, 0),
+    ("c3 smollm2-135m dim576 9/3 hd64 30L msl2048", 576, 9, 3, 30, 2048, 1e5, 512, 256, 0),
+    ("c4 llama3-8b dim4096 32/8 hd128 1L msl8192", 4096, 32, 8, 1, 8192, 5e5, 4096, 128, 0),
+    ("c5 llama3-8b long 1L, 131072 pre-filled", 4096, 32, 8, 1, 131136, 5e5, 0, 64, 131072),
+]
+
+
+def bench_workloads(torch, P) -> list:
+    """Each configuration end to end on device pointers: per layer one prefill
+    of P rows then D decode steps, timed once after one untimed pass."""
+    out = []
+    for name, dim, h, kvh, layers, msl, theta, npf, nd, pre in WORKLOADS:
+        hd = dim // h
+        kvd = hd * kvh
+        ctx = P.AttentionContext(dim, h, kvh, msl, layers, theta)
+        stream = torch.cuda.current_stream()
+        ctx.set_stream(stream.cuda_stream)
+        if pre:
+            fill_cache(torch, ctx, layers, msl, pre, 7)
+        rows = npf + nd
+        q = torch.randn(layers, rows, dim, device="cuda") * 0.5
+        k = torch.randn(layers, rows, kvd, device="cuda") * 0.5
+        v = torch.randn(layers, rows, kvd, device="cuda") * 0.5
+        o = torch.empty(layers, rows, dim, device="cuda")
+
+        def run():
+            for l in range(layers):
+                if npf:
+                    ctx.prefill_dev(l, pre, npf, q[l].data_ptr(), k[l].data_ptr(),
+                                    v[l].data_ptr(), o[l].data_ptr())
+                for st in range(nd):
+                    r = npf + st
+                    ctx.decode_dev(l, pre + r, q[l, r].data_ptr(), k[l, r].data_ptr(),
+                                   v[l, r].data_ptr(), o[l, r].data_ptr())
+
+        run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        flops = layers * 4 * hd * h * sum(range(pre + 1, pre + npf + 1))
+        dec_bytes = layers * sum(4 * (2 * (p + 1) * kvd + 2 * dim + 4 * kvd)
+                                 for p in range(pre + npf, pre + npf + nd))
+        out.append({"workload": name, "gpu_ms": round(ms, 4), "prefill_flops": flops,
+                    "decode_bytes": dec_bytes, "launches": layers * ((1 if npf else 0) + nd)})
+        ctx.close()
+        del q, k, v, o
+    return out
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """The oracle's decode (rope + append + JIT-softmax attention) at position
     32767 of one layer of the same shape, on one host core, repeated until
@@ -341,6 +398,8 @@ def main() -> int:
         log(f"prefill 4096: {pf['ms']:.3f} ms, {pf['tflops']:.2f} TFLOP/s")
         log("decode @131k")
         dl = bench_decode_131k(torch, P)
+        log("all configurations")
+        wl = bench_workloads(torch, P)
         log(f"decode @131k: {dl['ms_per_step']*1e3:.1f} us/step, {dl['gbs']:.1f} GB/s")
         extra = {
             "prefill_4k": {
@@ -354,6 +413,7 @@ def main() -> int:
                 "frac_hbm": dl["gbs"] / HBM_PEAK_GBS,
                 "workload": "64 decode steps at positions 131072..131135, 1 layer, 1 GiB KV",
             },
+            "configs": wl,
         }
     cpu = None
     if args.cpu_seconds > 0:
