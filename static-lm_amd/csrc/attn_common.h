@@ -58,6 +58,36 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// Max / sum over lanes l, l^16, l^32, l^48 (the four 16-lane rows of the
+// wave) with the VALU lane swaps of gfx950: each swap leaves x[l] and its
+// partner's value in the two outputs, in one order or the other, so the max
+// (sum) of the outputs is the pairwise max (sum).
+__device__ __forceinline__ float rows_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Online softmax keeps a running max m with the invariant l = sum 2^(s-m),
+// o = sum 2^(s-m) v.  The state is rescaled only when some lane's max has
+// grown by more than kLazyRescale (log2 units) since m was last set: below
+// that the stale m is kept, so terms are at most 2^8 and the rescale (one
+// multiply per accumulator element) is skipped for the whole wave.  Any m
+// satisfies the invariant, so the normalised result is unchanged.
+constexpr float kLazyRescale = 8.0f;
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
@@ -84,7 +114,7 @@ template <> struct LaneCfg<256> { static constexpr int LPG = 16; };
 
 // One online-softmax step of a lane group over TP positions (log2 domain):
 // scores q.k for GB heads reduced over the LPG lanes of the group, running
-// max m, running sum l, accumulator o rescaled by 2^(m_old - m_new).
+// max m, running sum l, accumulator o (lazy rescale, see kLazyRescale).
 // Positions with valid[tp] false contribute nothing.
 template <int LPG, int NV, int GB, int TP>
 __device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
@@ -111,9 +141,21 @@ __device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
         float mx = sc[0];
 #pragma unroll
         for (int tp = 1; tp < TP; ++tp) mx = fmaxf(mx, sc[tp]);
-        const float mn = fmaxf(m[i], mx);
-        const float mu = (mn == -INFINITY) ? 0.0f : mn;
-        const float alpha = fast_exp2(m[i] - mu);
+        if (__any(mx > m[i] + kLazyRescale)) {  // wave-uniform
+            const float mn = fmaxf(m[i], mx);
+            const float mu = (mn == -INFINITY) ? 0.0f : mn;
+            const float alpha = fast_exp2(m[i] - mu);
+            l[i] *= alpha;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                o[i][v].x *= alpha;
+                o[i][v].y *= alpha;
+                o[i][v].z *= alpha;
+                o[i][v].w *= alpha;
+            }
+            m[i] = mn;
+        }
+        const float mu = (m[i] == -INFINITY) ? 0.0f : m[i];
         float pr[TP];
         float ps = 0.0f;
 #pragma unroll
@@ -121,14 +163,10 @@ __device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
             pr[tp] = fast_exp2(sc[tp] - mu);
             ps += pr[tp];
         }
-        l[i] = l[i] * alpha + ps;
+        l[i] += ps;
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             float4 acc = o[i][v];
-            acc.x *= alpha;
-            acc.y *= alpha;
-            acc.z *= alpha;
-            acc.w *= alpha;
 #pragma unroll
             for (int tp = 0; tp < TP; ++tp) {
                 acc.x = fmaf(pr[tp], vr[tp][v].x, acc.x);
@@ -138,7 +176,6 @@ __device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
             }
             o[i][v] = acc;
         }
-        m[i] = mn;
     }
 }
 

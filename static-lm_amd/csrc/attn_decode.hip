@@ -39,25 +39,30 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxSplits = 1024;
 
 // Decode tiling per head_dim: lanes per position (LPG, 8 floats per lane
-// where head_dim allows) and positions per lane group per loop iteration
-// (TP).  Measured on MI355X for hd 128 at 32k and 131k context: 16 lanes x
-// 8 floats with one position per iteration keeps registers low enough
-// (~124 VGPRs) for several waves per SIMD and beat 8 lanes x 16 floats by
-// 5-7 points of HBM bandwidth.
+// where head_dim allows), positions per lane group per loop iteration (TP)
+// and waves per workgroup (NW).  Measured on MI355X for hd 128 at 32k and
+// 131k context: 16 lanes x 8 floats with one position per iteration keeps
+// registers low (~110 VGPRs) and beat 8 lanes x 16 floats by 5-7 points of
+// HBM bandwidth; what matters beyond that is two waves per SIMD, which
+// 4-wave x 512 and 8-wave x 256 workgroups reach equally (interleaved
+// medians 46 us at 32k, 153 us at 131k); 8 waves halve the splits to merge.
 template <int HD>
 struct DecodeCfg;
-template <> struct DecodeCfg<16> { static constexpr int LPG = 2, TP = 2; };
-template <> struct DecodeCfg<32> { static constexpr int LPG = 4, TP = 2; };
-template <> struct DecodeCfg<48> { static constexpr int LPG = 4, TP = 2; };
-template <> struct DecodeCfg<64> { static constexpr int LPG = 8, TP = 2; };
-template <> struct DecodeCfg<96> { static constexpr int LPG = 8, TP = 2; };
-template <> struct DecodeCfg<128> { static constexpr int LPG = 16, TP = 1; };
-template <> struct DecodeCfg<256> { static constexpr int LPG = 32, TP = 1; };
+template <> struct DecodeCfg<16> { static constexpr int LPG = 2, TP = 2, NW = 4; };
+template <> struct DecodeCfg<32> { static constexpr int LPG = 4, TP = 2, NW = 4; };
+template <> struct DecodeCfg<48> { static constexpr int LPG = 4, TP = 2, NW = 4; };
+template <> struct DecodeCfg<64> { static constexpr int LPG = 8, TP = 2, NW = 4; };
+template <> struct DecodeCfg<96> { static constexpr int LPG = 8, TP = 2, NW = 4; };
+template <> struct DecodeCfg<128> { static constexpr int LPG = 16, TP = 1, NW = 8; };
+template <> struct DecodeCfg<256> { static constexpr int LPG = 32, TP = 1, NW = 8; };
 
 template <int HD>
 constexpr int dec_span() {
-    return kWaves * (64 / DecodeCfg<HD>::LPG) * DecodeCfg<HD>::TP;
+    return DecodeCfg<HD>::NW * (64 / DecodeCfg<HD>::LPG) * DecodeCfg<HD>::TP;
 }
+
+// Waves one decode launch aims for on long sequences: two per SIMD.
+constexpr int kTargetWaves = 2048;
 
 struct DecodeParams {
     const float* q;      // [dim]; rotated at p here when cos_t != nullptr
@@ -83,7 +88,7 @@ struct DecodeParams {
 // Tiling of decode_kernel: lanes per position (LPG), positions per lane group
 // per loop iteration (TP) and waves per workgroup (NW).
 template <int HD, int GB, int LPG_ = DecodeCfg<HD>::LPG, int TP_ = DecodeCfg<HD>::TP,
-          int NW = kWaves>
+          int NW = DecodeCfg<HD>::NW>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     constexpr int LPG = LPG_;
     constexpr int FPL = HD / LPG;
@@ -325,8 +330,8 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
 template <int HD, int GB>
 hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st) {
     const int groups = s.num_kv_heads * (s.kv_mul / GB);
-    hipLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups), dim3(kThreads),
-                       0, st, dp);
+    hipLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups),
+                       dim3(64 * DecodeCfg<HD>::NW), 0, st, dp);
     return hipGetLastError();
 }
 
@@ -345,6 +350,19 @@ hipError_t launch_hd(const Shape& s, const DecodeParams& dp, hipStream_t st) {
         case 3: return launch_t<HD, 3>(s, dp, st);
         case 2: return launch_t<HD, 2>(s, dp, st);
         default: return launch_t<HD, 1>(s, dp, st);
+    }
+}
+
+int decode_waves(const Shape& s) {
+    switch (s.head_dim) {
+        case 16: return DecodeCfg<16>::NW;
+        case 32: return DecodeCfg<32>::NW;
+        case 48: return DecodeCfg<48>::NW;
+        case 64: return DecodeCfg<64>::NW;
+        case 96: return DecodeCfg<96>::NW;
+        case 128: return DecodeCfg<128>::NW;
+        case 256: return DecodeCfg<256>::NW;
+        default: return kWaves;
     }
 }
 
@@ -368,12 +386,14 @@ int decode_groups(const Shape& s) { return s.num_kv_heads * (s.kv_mul / pick_gb(
 int decode_max_splits() { return kMaxSplits; }
 
 void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* chunk) {
-    // About 512 workgroups (two per CU) on long sequences, each walking at
-    // least 8 loop iterations, at most kMaxSplits splits.  A pure function of
-    // seq_len and the shape, so results reproduce run to run.
+    // About kTargetWaves waves (two per SIMD) on long sequences, each
+    // workgroup walking at least 8 loop iterations, at most kMaxSplits splits.
+    // A pure function of seq_len and the shape, so results reproduce run to
+    // run.
     const int it = decode_span(s);
     const int groups = decode_groups(s);
-    const int want = groups >= 512 ? 1 : 512 / groups;
+    const int wgs = kTargetWaves / decode_waves(s);
+    const int want = groups >= wgs ? 1 : wgs / groups;
     int c = (seq_len + want - 1) / want;
     if (c < 8 * it) c = 8 * it;
     c = (c + it - 1) / it * it;

@@ -219,24 +219,27 @@ prefill_mfma_kernel(PrefillParams p) {
                     mx = fmaxf(mx, v);
                 }
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mn = fmaxf(m[qt], mx);
-            const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
-            m[qt] = mn;
+            mx = rows_max(mx);
+            // the first tile always holds key 0 <= qpos, so m is finite after it
+            if (__any(mx > m[qt] + kLazyRescale)) {  // wave-uniform
+                const float mn = fmaxf(m[qt], mx);
+                const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
+                l[qt] *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+                m[qt] = mn;
+            }
             float ps = 0.0f;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float e = __builtin_amdgcn_exp2f(s[ks][qt][r] - mn);
+                    const float e = __builtin_amdgcn_exp2f(s[ks][qt][r] - m[qt]);
                     s[ks][qt][r] = e;
                     ps += e;
                 }
             }
-            l[qt] = l[qt] * alpha + ps;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+            l[qt] += ps;
         }
 
         // O^T += V^T . P^T
@@ -261,9 +264,7 @@ prefill_mfma_kernel(PrefillParams p) {
     // normalise and store: lane holds out[row q0+qt*16+lr][dt*16 + 4*lg .. +3]
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
-        float lt = l[qt];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
+        const float lt = rows_sum(l[qt]);
         const int row = q0 + qt * 16 + lr;
         if (row < p.n) {
             const float inv = 1.0f / lt;
