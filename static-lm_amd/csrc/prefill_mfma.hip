@@ -319,8 +319,8 @@ hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
 
 }  // namespace
 
-bool prefill_mfma_supported(const Shape& s) {
-    switch (s.head_dim) {
+bool head_dim_supported(int hd) {
+    switch (hd) {
         case 16: case 32: case 48: case 64: case 96: case 128: case 256:
             return true;
         default:

@@ -290,21 +290,11 @@ int do_attend(slm_attn_ctx* c, int layer, int start, int n, const float* q,
               float* out, bool rotate) {
     const slm::Shape& s = c->shape;
     if (n == 1) return do_decode(c, layer, start, q, nullptr, nullptr, out, rotate);
-    Timed t(c, SLM_K_PREFILL);
-    hipError_t e;
-    if (slm::prefill_mfma_supported(s)) {
-        slm::PrefillArgs pa{q,          k_base(c, layer), v_base(c, layer),
-                            rotate ? c->cos_t : nullptr,
-                            rotate ? c->sin_t : nullptr, out, start, n};
-        e = slm::launch_prefill_mfma(s, pa, c->stream);
-    } else {
-        slm::RowsArgs a{q,   k_base(c, layer),
-                        v_base(c, layer),
+    slm::PrefillArgs pa{q,          k_base(c, layer), v_base(c, layer),
                         rotate ? c->cos_t : nullptr,
-                        rotate ? c->sin_t : nullptr,
-                        out, start, n};
-        e = slm::launch_attn_rows(s, a, c->stream);
-    }
+                        rotate ? c->sin_t : nullptr, out, start, n};
+    Timed t(c, SLM_K_PREFILL);
+    hipError_t e = slm::launch_prefill_mfma(s, pa, c->stream);
     t.done();
     return launch_status(c, e, "prefill kernel launch");
 }

@@ -30,19 +30,6 @@ hipError_t launch_kv_append(const Shape& s, const float* k, const float* v,
 hipError_t launch_rope(const Shape& s, float* x, int n, int row_len, int pos0,
                        const float* cos_t, const float* sin_t, hipStream_t st);
 
-// Batched attention rows, one workgroup per (row, KV head x head batch)
-// walking the row's whole causal range (no split).
-struct RowsArgs {
-    const float* q;        // [rows][dim], head h at h*head_dim
-    const float* k_cache;  // layer K base, [max_seq_len][kv_dim]
-    const float* v_cache;  // layer V base
-    const float* cos_t;    // RoPE tables, or nullptr when q is already rotated
-    const float* sin_t;
-    float* out;            // [rows][dim]
-    int start;             // row r sits at position start + r
-    int rows;
-};
-hipError_t launch_attn_rows(const Shape& s, const RowsArgs& a, hipStream_t st);
 bool head_dim_supported(int head_dim);
 
 // Single-token decode: optional KV append at pos fused into split-K
@@ -82,7 +69,6 @@ struct PrefillArgs {
     int start;
     int n;
 };
-bool prefill_mfma_supported(const Shape& s);
 hipError_t launch_prefill_mfma(const Shape& s, const PrefillArgs& a,
                                hipStream_t st);
 
