@@ -149,7 +149,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
     avg_split_s = split_ms / max(n_split, 1) / 1e3
     kv_bytes = 2 * (pos + 1) * KV_DIM * 4
     achieved = kv_bytes / avg_split_s / 1e9
-    ns, chunk = ctx.decode_splits(pos + 1)
+    ns, tile = ctx.decode_splits(pos + 1)
     finite = bool(torch.isfinite(out).all().item())
     ctx.close()
     step_bytes = layers * decode_bytes(pos)
@@ -158,7 +158,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
         "step_bytes": step_bytes, "gbs": step_bytes * steps / (ms / 1e3) / 1e9,
         "profile": prof, "split_kernel_avg_us": avg_split_s * 1e6,
         "split_kernel_bytes": kv_bytes, "split_kernel_gbs": achieved,
-        "splits": ns, "chunk": chunk, "finite": finite,
+        "splits": ns, "tile": tile, "finite": finite,
         "combine_avg_us": comb_ms / max(n_comb, 1) * 1e3,
     }
 
@@ -439,7 +439,7 @@ def main() -> int:
                         "head_dim 128), 8 layers of f32 KV rotated per step",
             "dim": DIM, "num_heads": HEADS, "num_kv_heads": KV_HEADS, "head_dim": HD,
             "ctx": d["pos"] + 1, "layers": d["layers"], "rope_theta": THETA,
-            "bytes_per_step": d["step_bytes"], "splits": d["splits"], "chunk": d["chunk"],
+            "bytes_per_step": d["step_bytes"], "splits": d["splits"], "split_tile": d["tile"],
         },
         "roofline": {
             "bound": "hbm",

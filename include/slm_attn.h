@@ -190,11 +190,12 @@ typedef struct slm_kernel_stat {
 int slm_attn_profile(slm_attn_ctx* ctx, int32_t enable);
 int slm_attn_profile_read(slm_attn_ctx* ctx, slm_kernel_stat* out /* [SLM_K_COUNT] */);
 
-/* Number of split-K chunks and chunk length the decode kernel uses at a given
- * sequence length (a pure function of seq_len and the config, so results
- * reproduce run to run). */
+/* Split-K layout the decode kernel uses at a given sequence length: positions
+ * are cut into tiles of *tile rows and split s of *n_splits reads tiles s,
+ * s + n_splits, s + 2*n_splits, ...  A pure function of seq_len, the config and
+ * the device's CU count, so results reproduce run to run on a device. */
 int slm_attn_decode_splits(const slm_attn_ctx* ctx, int32_t seq_len,
-                           int32_t* n_splits, int32_t* chunk);
+                           int32_t* n_splits, int32_t* tile);
 
 /* Library version string. */
 const char* slm_attn_version(void);

@@ -306,10 +306,11 @@ class AttentionContext:
                 for i, name in enumerate(KERNEL_KINDS)}
 
     def decode_splits(self, seq_len: int) -> tuple[int, int]:
-        ns, ch = _I(), _I()
+        """(n_splits, tile): split s reads tiles s, s + n_splits, ... of `tile` rows."""
+        ns, tile = _I(), _I()
         self._check(self.lib.slm_attn_decode_splits(self._h, seq_len, ctypes.byref(ns),
-                                                    ctypes.byref(ch)))
-        return ns.value, ch.value
+                                                    ctypes.byref(tile)))
+        return ns.value, tile.value
 
 
 def header_functions(header: os.PathLike | str = HEADER_PATH) -> list[str]:

@@ -9,8 +9,13 @@
 //
 // Mapping.  blockIdx.x = split * groups + group, so workgroups that run at
 // the same time cover every KV head of the same positions (whole 4 KiB cache
-// rows for the Llama-3-8B shape).  A workgroup owns positions
-// [split*chunk, min(p+1, (split+1)*chunk)) of one KV head and GB of its
+// rows for the Llama-3-8B shape).  Positions 0..p are cut into tiles of IT
+// (the positions one loop iteration of a workgroup covers) and split s of n
+// takes tiles s, s+n, s+2n, ...: at any moment the n splits stream one
+// contiguous stretch of the cache, every split gets the same number of tiles
+// to within one, and no sequence length lines the splits up on a bad
+// address stride (contiguous chunks of 4128 rows ran at 74% of HBM peak
+// where 4096 rows ran at 89%).  A workgroup covers one KV head and GB of its
 // kv_mul query heads: each K/V segment loaded from HBM serves GB heads (the
 // reference re-reads it once per head).  In a wave, LPG lanes hold one
 // position's head_dim floats (128-bit nontemporal loads, LPG*16 contiguous
@@ -61,8 +66,8 @@ constexpr int dec_span() {
     return DecodeCfg<HD>::NW * (64 / DecodeCfg<HD>::LPG) * DecodeCfg<HD>::TP;
 }
 
-// Waves one decode launch aims for on long sequences: two per SIMD.
-constexpr int kTargetWaves = 2048;
+// Waves per CU one decode launch aims for on long sequences: two per SIMD.
+constexpr int kWavesPerCu = 8;
 
 struct DecodeParams {
     const float* q;      // [dim]; rotated at p here when cos_t != nullptr
@@ -76,7 +81,6 @@ struct DecodeParams {
     float* part_o;       // [n_splits][num_heads][head_dim]
     float* part_ml;      // [n_splits][num_heads][2]
     int pos;
-    int chunk;
     int n_splits;
     int num_heads;
     int kv_dim;
@@ -105,11 +109,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     const int g = gy / nhb;
     const int h0 = g * p.kv_mul + (gy % nhb) * GB;
     const int seq_len = p.pos + 1;
-    const int t0 = split * p.chunk;
-    const int t1 = min(seq_len, t0 + p.chunk);
+    const int t0 = split * IT;
+    const int t_step = p.n_splits * IT;
     const bool append = p.k_new != nullptr;
-    const bool owner = t1 == seq_len;
-    const int t_end = (append && owner) ? p.pos : t1;  // rows read from the cache
+    const bool owner = (p.pos / IT) % p.n_splits == split;  // holds row p's tile
+    const int t_end = append ? p.pos : seq_len;  // rows read from the cache
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -126,7 +130,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int tp = 0; tp < TP; ++tp) {
             const int t = tb + (tp * NW + wave) * GPW + lg;
             valid[tp] = t < t_end;
-            const long tt = valid[tp] ? t : t0;
+            const long tt = valid[tp] ? t : 0;
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
                 kr[tp][v] = ld4_stream(kbase + tt * p.kv_dim + 4 * v * LPG);
@@ -201,7 +205,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         }
     }
 
-    for (int tb = t0; tb < t_end; tb += IT) {
+    for (int tb = t0; tb < t_end; tb += t_step) {
         if (tb != t0) load_tile(tb);
         attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
     }
@@ -252,12 +256,21 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     }
 }
 
-// Log-sum-exp merge of the split partials: one workgroup per (head, 64 head
-// dims).  The partial accumulators of a round of up to 64 splits are loaded
-// before the split weights are known, so a round costs one memory latency.
+// Head dims one combine workgroup merges: a divisor of head_dim, at most one
+// per lane (hd 96 takes three workgroups of 32).
+template <int HD>
+constexpr int combine_width() {
+    return HD <= 64 ? HD : (HD % 64 == 0 ? 64 : 32);
+}
+
+// Log-sum-exp merge of the split partials: one workgroup per (head,
+// combine_width head dims).  The partial accumulators of a round of up to 64
+// splits are loaded before the split weights are known, so a round costs one
+// memory latency.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p) {
-    constexpr int DW = HD < 64 ? HD : 64;  // head dims per workgroup
+    constexpr int DW = combine_width<HD>();  // head dims per workgroup
+    static_assert(HD % DW == 0 && DW <= 64, "combine workgroups must tile head_dim");
     constexpr int U = 16;                   // splits per wave per round
     __shared__ float s_w[kMaxSplits];
     __shared__ float s_acc[kWaves][DW];
@@ -337,7 +350,7 @@ hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st) {
 
 template <int HD>
 hipError_t launch_combine_t(const Shape& s, const DecodeParams& dp, hipStream_t st) {
-    constexpr int DW = HD < 64 ? HD : 64;
+    constexpr int DW = combine_width<HD>();
     hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads, HD / DW), dim3(kThreads), 0,
                        st, dp);
     return hipGetLastError();
@@ -385,30 +398,28 @@ int decode_groups(const Shape& s) { return s.num_kv_heads * (s.kv_mul / pick_gb(
 
 int decode_max_splits() { return kMaxSplits; }
 
-void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* chunk) {
-    // About kTargetWaves waves (two per SIMD) on long sequences, each
-    // workgroup walking at least 8 loop iterations, at most kMaxSplits splits.
-    // A pure function of seq_len and the shape, so results reproduce run to
-    // run.
+void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* tile) {
+    // Two waves per SIMD on long sequences (for 8-wave workgroups, one per
+    // CU: a launch with a few workgroups more than CUs doubles some CUs up
+    // and measured 20-30% slower), each split walking at least 8 tiles, at
+    // most kMaxSplits splits.  A pure function of seq_len, the shape and the
+    // CU count, so results reproduce run to run on a device.
     const int it = decode_span(s);
     const int groups = decode_groups(s);
-    const int wgs = kTargetWaves / decode_waves(s);
+    const int wgs = kWavesPerCu * s.cus / decode_waves(s);
     const int want = groups >= wgs ? 1 : wgs / groups;
-    int c = (seq_len + want - 1) / want;
-    if (c < 8 * it) c = 8 * it;
-    c = (c + it - 1) / it * it;
-    if ((seq_len + c - 1) / c > kMaxSplits) {
-        c = (seq_len + kMaxSplits - 1) / kMaxSplits;
-        c = (c + it - 1) / it * it;
-    }
-    *chunk = c;
-    *n_splits = (seq_len + c - 1) / c;
+    const int tiles = (seq_len + it - 1) / it;
+    int ns = tiles / 8 < want ? tiles / 8 : want;
+    if (ns < 1) ns = 1;
+    if (ns > kMaxSplits) ns = kMaxSplits;
+    *n_splits = ns;
+    *tile = it;
 }
 
 static DecodeParams decode_params(const Shape& s, const DecodeArgs& a) {
     return DecodeParams{a.q,        a.k_new,   a.v_new,     a.k_cache,  a.v_cache,
                     a.cos_t,    a.sin_t,   a.out,       a.part_o,   a.part_ml,
-                    a.pos,      a.chunk,   a.n_splits,  s.num_heads,
+                    a.pos,      a.n_splits,  s.num_heads,
                     s.kv_dim,   s.kv_mul,  s.half,
                     1.4426950408889634f / sqrtf((float)s.head_dim)};
 }

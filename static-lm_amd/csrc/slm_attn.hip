@@ -256,8 +256,8 @@ int do_append(slm_attn_ctx* c, int layer, int pos0, int n, const float* k,
 int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* k_new,
               const float* v_new, float* out, bool rotate) {
     const slm::Shape& s = c->shape;
-    int ns = 1, chunk = 1;
-    slm::decode_split_policy(s, pos + 1, &ns, &chunk);
+    int ns = 1, tile = 1;
+    slm::decode_split_policy(s, pos + 1, &ns, &tile);
     slm::DecodeArgs a{q,
                       k_new,
                       v_new,
@@ -269,7 +269,6 @@ int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* 
                       c->part_o,
                       c->part_ml,
                       pos,
-                      chunk,
                       ns};
     {
         Timed t(c, SLM_K_DECODE);
@@ -362,6 +361,7 @@ int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
     s.kv_mul = cfg->num_heads / cfg->num_kv_heads;
     s.half = hd / 2;
     s.max_seq_len = cfg->max_seq_len;
+    s.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
 
     auto bail = [&](int code) {
         slm_attn_destroy(c);
@@ -391,8 +391,8 @@ int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
 
     int max_splits = 1;
     for (int len = 1; len <= cfg->max_seq_len; ++len) {
-        int ns = 1, chunk = 1;
-        slm::decode_split_policy(s, len, &ns, &chunk);
+        int ns = 1, tile = 1;
+        slm::decode_split_policy(s, len, &ns, &tile);
         if (ns > max_splits) max_splits = ns;
     }
     c->max_splits = max_splits;
@@ -666,13 +666,13 @@ int slm_attn_profile_read(slm_attn_ctx* c, slm_kernel_stat* out) {
 }
 
 int slm_attn_decode_splits(const slm_attn_ctx* c, int32_t seq_len,
-                           int32_t* n_splits, int32_t* chunk) {
-    if (!c || !n_splits || !chunk || seq_len <= 0)
+                           int32_t* n_splits, int32_t* tile) {
+    if (!c || !n_splits || !tile || seq_len <= 0)
         return fail(nullptr, SLM_ERR_ARG, "bad argument");
-    int ns = 1, ch = 1;
-    slm::decode_split_policy(c->shape, seq_len, &ns, &ch);
+    int ns = 1, t = 1;
+    slm::decode_split_policy(c->shape, seq_len, &ns, &t);
     *n_splits = ns;
-    *chunk = ch;
+    *tile = t;
     return SLM_OK;
 }
 

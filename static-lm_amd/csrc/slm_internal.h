@@ -17,6 +17,7 @@ struct Shape {
     int kv_mul;
     int half;  // head_dim / 2, the RoPE table row length
     int max_seq_len;
+    int cus;   // compute units of the device (sizes the decode split count)
 };
 
 // K/V append: rows pos0..pos0+n-1 of the layer's K slice get rope(k row),
@@ -46,11 +47,12 @@ struct DecodeArgs {
     float* part_o;       // [n_splits][num_heads][head_dim]
     float* part_ml;      // [n_splits][num_heads][2]
     int pos;
-    int chunk;
     int n_splits;
 };
-// n_splits and chunk as a pure function of seq_len and the shape.
-void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* chunk);
+// Split count and tile length (positions) at seq_len: split s of n reads
+// tiles s, s+n, s+2n, ...  A pure function of seq_len, the shape and the CU
+// count.
+void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* tile);
 int decode_groups(const Shape& s);
 int decode_max_splits();
 hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st);

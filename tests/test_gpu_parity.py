@@ -165,8 +165,8 @@ def test_decode_deterministic_and_split_invariant():
     w = WORKLOADS["c4"]
     pos = 6000
     with make_ctx(w) as ctx:
-        ns, chunk = ctx.decode_splits(pos + 1)
-        log(f"splits at {pos + 1}: {ns} x {chunk}")
+        ns, tile = ctx.decode_splits(pos + 1)
+        log(f"splits at {pos + 1}: {ns}, tiles of {tile} rows")
         assert ns > 1
         for p0 in range(0, pos + 1, 2048):
             m = min(2048, pos + 1 - p0)
@@ -348,3 +348,58 @@ def test_prefill_shapes_and_ragged_batches(dim, heads, kv_heads, start, n):
             if b < n:
                 assert_close(g[b], om.attend(0, q[start + b], start + b),
                              what=f"row {b} at {start + b}")
+
+
+DECODE_SHAPES = [
+    (64, 4, 4),      # hd 16
+    (256, 8, 2),     # hd 32, kv_mul 4
+    (288, 6, 6),     # hd 48
+    (576, 9, 3),     # hd 64, kv_mul 3
+    (768, 8, 8),     # hd 96
+    (4096, 32, 8),   # hd 128, kv_mul 4 (Llama-3-8B)
+    (2048, 16, 2),   # hd 128, kv_mul 8
+    (1024, 4, 4),    # hd 256
+]
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads", DECODE_SHAPES)
+def test_decode_split_tiles_across_shapes(dim, heads, kv_heads):
+    """Decode with append at positions where split ownership changes.
+
+    Split s reads tiles s, s+n, ... of the cache; the split holding row p's tile
+    writes row p and seeds its state with it.  Positions: the first row of a
+    tile held by split 0 and by split 1, the last row of the last split's tile,
+    and a row inside another split's tile.
+    """
+    msl = 6000
+    cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, 1e4)
+    kvd = cfg.kv_dim
+    om = orc.OracleModel(cfg)
+    with P.AttentionContext(dim, heads, kv_heads, msl, 1) as ctx:
+        picks = {}
+        for p in range(4200, msl - 1):
+            ns, tile = ctx.decode_splits(p + 1)
+            assert ns > 1
+            owner, row = (p // tile) % ns, p % tile
+            for key, at in (("split 0 tile start", (0, 0)), ("split 1 tile start", (1, 0)),
+                            ("last split, last row", (ns - 1, tile - 1)),
+                            ("another split", (min(3, ns - 1), 5 % tile))):
+                if (owner, row) == at and key not in picks:
+                    picks[key] = p
+        assert len(picks) == 4, picks
+        cands = sorted(set(picks.values()))
+        log(f"decode shape dim {dim} heads {heads}/{kv_heads}: positions {picks}")
+        top = cands[-1]
+        kr = gen([81, dim], (top, kvd))
+        vr = gen([82, dim], (top, kvd))
+        ctx.kv_write(0, 0, 0, kr)
+        ctx.kv_write(0, 1, 0, vr)
+        om.k_cache(0)[:top] = kr
+        om.v_cache(0)[:top] = vr
+        for p in cands:
+            q1, k1, v1 = gen([83, p], dim), gen([84, p], kvd), gen([85, p], kvd)
+            g = ctx.decode(0, p, q1, k1, v1)
+            r = om.decode(0, p, q1, k1, v1)
+            assert_close(g, r, what=f"decode at {p}")
+            assert_bitwise(ctx.kv_read(0, 0, p, 1), om.k_cache(0)[p:p + 1], f"K row {p}")
+            assert_bitwise(ctx.kv_read(0, 1, p, 1), om.v_cache(0)[p:p + 1], f"V row {p}")
