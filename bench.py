@@ -352,6 +352,9 @@ def main() -> int:
                     help="time budget of the CPU baseline sample (0 skips it)")
     ap.add_argument("--skip-extra", action="store_true",
                     help="only the headline decode @32k measurement")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the 4096-row prefill (a short program for counter passes); "
+                         "prints its own JSON line, not the headline one")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB: a plain "
                          "copy kernel of known size that scales rocprofv3 byte counters")
@@ -387,6 +390,13 @@ def main() -> int:
             f"{args.copy_calibration_mib} MiB written")
         del src, dst
 
+    if args.prefill_only:
+        pf = bench_prefill_4k(torch, P, reps=max(3, args.steps // 10))
+        log(f"prefill 4096: {pf['ms']:.3f} ms, {pf['tflops']:.2f} TFLOP/s")
+        print(json.dumps({"prefill_4k_tflops": pf["tflops"], "ms": pf["ms"],
+                          "kernel_avg_ms": pf["kernel_avg_ms"]}))
+        return 0
+
     log("decode @32k")
     d = bench_decode_32k(torch, P, args.steps, args.warmup)
     log(f"decode @32k: {d['gbs']:.1f} GB/s, split kernel {d['split_kernel_avg_us']:.1f} us "
@@ -401,7 +411,20 @@ def main() -> int:
         log("all configurations")
         wl = bench_workloads(torch, P)
         log(f"decode @131k: {dl['ms_per_step']*1e3:.1f} us/step, {dl['gbs']:.1f} GB/s")
+        log("calibration")
+        cal_mfma = P.calibrate_mfma_f32(iters=20000)
+        cal_nt = P.calibrate_hbm_read(4 << 30, nontemporal=True)
+        cal_plain = P.calibrate_hbm_read(4 << 30, nontemporal=False)
+        log(f"calibration: fp32 MFMA {cal_mfma['tflops']:.1f} TFLOP/s, HBM read "
+            f"{cal_nt:.0f} GB/s nontemporal, {cal_plain:.0f} GB/s plain")
         extra = {
+            "calibration": {
+                "mfma_f32_16x16x4_tflops": round(cal_mfma["tflops"], 2),
+                "hbm_read_nontemporal_gbs": round(cal_nt, 1),
+                "hbm_read_plain_gbs": round(cal_plain, 1),
+                "note": "measured ceilings on this device (slm_calib.h); roofline.peak stays "
+                        "the published figure",
+            },
             "prefill_4k": {
                 "tflops": pf["tflops"], "ms": pf["ms"], "flops": pf["flops"],
                 "frac_fp32_mfma": pf["tflops"] / FP32_MFMA_PEAK_TFLOPS,
@@ -443,7 +466,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel<128,4> (append + split-K decode)",
+            "kernel": "decode_kernel<128,4,16,1,8> (append + interleaved split-K decode)",
             "achieved": round(d["split_kernel_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

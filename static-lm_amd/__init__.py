@@ -24,6 +24,7 @@ import numpy as np
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libslm_attn.so"
 HEADER_PATH = PKG_DIR.parent / "include" / "slm_attn.h"
+CALIB_HEADER_PATH = PKG_DIR.parent / "include" / "slm_calib.h"
 
 SLM_OK = 0
 ERRORS = {
@@ -118,6 +119,11 @@ SIGNATURES = {
     "slm_attn_profile_read": (ctypes.c_int, [_P, ctypes.POINTER(_KernelStat)]),
     "slm_attn_decode_splits": (ctypes.c_int, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "slm_attn_version": (ctypes.c_char_p, []),
+    # slm_calib.h
+    "slm_calib_mfma_f32": (ctypes.c_int, [_I, _I, ctypes.POINTER(ctypes.c_double),
+                                          ctypes.POINTER(ctypes.c_double)]),
+    "slm_calib_hbm_read": (ctypes.c_int, [_I, ctypes.c_int64, _I,
+                                          ctypes.POINTER(ctypes.c_double)]),
 }
 
 _lib = None
@@ -313,9 +319,32 @@ class AttentionContext:
         return ns.value, tile.value
 
 
-def header_functions(header: os.PathLike | str = HEADER_PATH) -> list[str]:
-    """Names of the functions include/slm_attn.h declares."""
+def header_functions(*headers: os.PathLike | str) -> list[str]:
+    """Names of the functions the given headers (default: every include/*.h) declare."""
     import re
 
-    text = Path(header).read_text()
-    return sorted(set(re.findall(r"\b(slm_[a-z0-9_]+)\s*\(", text)))
+    paths = headers or (HEADER_PATH, CALIB_HEADER_PATH)
+    names = set()
+    for h in paths:
+        names |= set(re.findall(r"\b(slm_[a-z0-9_]+)\s*\(", Path(h).read_text()))
+    return sorted(names)
+
+
+def calibrate_mfma_f32(iters: int = 20000, device: int = 0) -> dict:
+    """Measured v_mfma_f32_16x16x4_f32 rate of the device (slm_calib_mfma_f32)."""
+    lib = load_library()
+    tf, ms = ctypes.c_double(), ctypes.c_double()
+    rc = lib.slm_calib_mfma_f32(device, iters, ctypes.byref(tf), ctypes.byref(ms))
+    if rc != SLM_OK:
+        raise SlmAttnError(rc, "slm_calib_mfma_f32 failed")
+    return {"tflops": tf.value, "ms": ms.value, "iters": iters}
+
+
+def calibrate_hbm_read(nbytes: int = 4 << 30, nontemporal: bool = True, device: int = 0) -> float:
+    """Measured streaming-read rate in GB/s (slm_calib_hbm_read)."""
+    lib = load_library()
+    gbs = ctypes.c_double()
+    rc = lib.slm_calib_hbm_read(device, nbytes, 1 if nontemporal else 0, ctypes.byref(gbs))
+    if rc != SLM_OK:
+        raise SlmAttnError(rc, "slm_calib_hbm_read failed")
+    return gbs.value

@@ -68,6 +68,8 @@ constexpr int dec_span() {
 
 // Waves per CU one decode launch aims for on long sequences: two per SIMD.
 constexpr int kWavesPerCu = 8;
+// Sequences of at most this many tiles run as one split (no merge launch).
+constexpr int kMinTilesToSplit = 8;
 
 struct DecodeParams {
     const float* q;      // [dim]; rotated at p here when cos_t != nullptr
@@ -399,18 +401,23 @@ int decode_groups(const Shape& s) { return s.num_kv_heads * (s.kv_mul / pick_gb(
 int decode_max_splits() { return kMaxSplits; }
 
 void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* tile) {
-    // Two waves per SIMD on long sequences (for 8-wave workgroups, one per
-    // CU: a launch with a few workgroups more than CUs doubles some CUs up
-    // and measured 20-30% slower), each split walking at least 8 tiles, at
-    // most kMaxSplits splits.  A pure function of seq_len, the shape and the
-    // CU count, so results reproduce run to run on a device.
+    // As many splits as there are tiles, up to two waves per SIMD (for
+    // 8-wave workgroups one per CU: a few workgroups more than CUs double
+    // some CUs up and measured 20-30% slower) and kMaxSplits.  Below that
+    // the kernel is latency-bound and every tile a split walks costs about
+    // one memory round trip, so one tile per split wins (Llama-3-8B shape at
+    // 4096 rows: 15.0 us with 32 splits against 17.4 us with 16; SmolLM2 at
+    // 768 rows: 10.8 us with 12 splits against 13.0 us with one).  Up to
+    // kMinTilesToSplit tiles the merge launch costs more than it saves, and
+    // a single split writes the output directly.  A pure function of
+    // seq_len, the shape and the CU count, so results reproduce run to run
+    // on a device.
     const int it = decode_span(s);
     const int groups = decode_groups(s);
     const int wgs = kWavesPerCu * s.cus / decode_waves(s);
     const int want = groups >= wgs ? 1 : wgs / groups;
     const int tiles = (seq_len + it - 1) / it;
-    int ns = tiles / 8 < want ? tiles / 8 : want;
-    if (ns < 1) ns = 1;
+    int ns = tiles <= kMinTilesToSplit ? 1 : (tiles < want ? tiles : want);
     if (ns > kMaxSplits) ns = kMaxSplits;
     *n_splits = ns;
     *tile = it;

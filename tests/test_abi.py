@@ -1,6 +1,6 @@
 """C-ABI checks that need no GPU: the library loads, exports every function
-include/slm_attn.h declares, and rejects bad arguments with the codes that
-mirror the reference's asserts before touching a device."""
+include/*.h declares, and rejects bad arguments with the codes that mirror the
+reference's asserts before touching a device."""
 import ctypes
 import subprocess
 
@@ -33,6 +33,9 @@ def test_version_and_null_handles():
     assert lib.slm_kv_offset(None, 0, 0, 0) == ctypes.c_size_t(-1).value
     assert lib.slm_kv_device_ptr(None) is None
     lib.slm_attn_destroy(None)  # no-op
+    # measurement helpers check their arguments before any HIP call
+    assert lib.slm_calib_mfma_f32(0, 0, None, None) == P.ERR_ARG
+    assert lib.slm_calib_hbm_read(0, 1 << 20, 1, None) == P.ERR_ARG
 
 
 @pytest.mark.parametrize("dim,heads,kv_heads,msl,layers,theta,why", [

@@ -366,29 +366,37 @@ DECODE_SHAPES = [
 def test_decode_split_tiles_across_shapes(dim, heads, kv_heads):
     """Decode with append at positions where split ownership changes.
 
-    Split s reads tiles s, s+n, ... of the cache; the split holding row p's tile
-    writes row p and seeds its state with it.  Positions: the first row of a
-    tile held by split 0 and by split 1, the last row of the last split's tile,
-    and a row inside another split's tile.
+    Split s of n reads tiles s, s+n, ... of the cache; the split holding row p's
+    tile writes row p and seeds its state with it.  While the split count is
+    below its cap there is one tile per split and the last split owns row p;
+    beyond it ownership rotates.  Positions: the shortest sequence that splits,
+    and, past the cap, the first row of a tile held by split 0 and by split 1,
+    the last row of the last split's tile, and a row inside another split's.
     """
-    msl = 6000
+    with P.AttentionContext(dim, heads, kv_heads, 16, 1) as probe:
+        cap, tile = probe.decode_splits(1 << 24)
+    msl = 2 * cap * tile + 2 * tile
     cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, 1e4)
     kvd = cfg.kv_dim
     om = orc.OracleModel(cfg)
     with P.AttentionContext(dim, heads, kv_heads, msl, 1) as ctx:
         picks = {}
-        for p in range(4200, msl - 1):
-            ns, tile = ctx.decode_splits(p + 1)
-            assert ns > 1
-            owner, row = (p // tile) % ns, p % tile
-            for key, at in (("split 0 tile start", (0, 0)), ("split 1 tile start", (1, 0)),
-                            ("last split, last row", (ns - 1, tile - 1)),
-                            ("another split", (min(3, ns - 1), 5 % tile))):
-                if (owner, row) == at and key not in picks:
-                    picks[key] = p
-        assert len(picks) == 4, picks
+        for p in range(msl - 1):
+            ns, t = ctx.decode_splits(p + 1)
+            assert t == tile
+            if ns == 1:
+                continue
+            picks.setdefault("shortest split sequence", p)
+            if ns < p // tile + 1:  # past the cap
+                owner, row = (p // tile) % ns, p % tile
+                for key, at in (("split 0 tile start", (0, 0)), ("split 1 tile start", (1, 0)),
+                                ("last split, last row", (ns - 1, tile - 1)),
+                                ("another split", (min(3, ns - 1), 5 % tile))):
+                    if (owner, row) == at:
+                        picks.setdefault(key, p)
+        assert len(picks) == 5, picks
         cands = sorted(set(picks.values()))
-        log(f"decode shape dim {dim} heads {heads}/{kv_heads}: positions {picks}")
+        log(f"decode shape dim {dim} heads {heads}/{kv_heads} msl {msl}: positions {picks}")
         top = cands[-1]
         kr = gen([81, dim], (top, kvd))
         vr = gen([82, dim], (top, kvd))
@@ -403,3 +411,12 @@ def test_decode_split_tiles_across_shapes(dim, heads, kv_heads):
             assert_close(g, r, what=f"decode at {p}")
             assert_bitwise(ctx.kv_read(0, 0, p, 1), om.k_cache(0)[p:p + 1], f"K row {p}")
             assert_bitwise(ctx.kv_read(0, 1, p, 1), om.v_cache(0)[p:p + 1], f"V row {p}")
+
+
+def test_calibration_helpers_report_plausible_rates():
+    r = P.calibrate_mfma_f32(iters=4000)
+    log(f"fp32 MFMA {r['tflops']:.1f} TFLOP/s")
+    assert 20.0 < r["tflops"] < 200.0
+    gbs = P.calibrate_hbm_read(1 << 30, nontemporal=True)
+    log(f"HBM read {gbs:.0f} GB/s")
+    assert 500.0 < gbs < 10000.0
