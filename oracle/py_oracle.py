@@ -33,6 +33,7 @@ _D = ctypes.POINTER(ctypes.c_double)
 _C = ctypes.POINTER(OrcConfig)
 _SZ = ctypes.c_size_t
 _I = ctypes.c_int
+_U8 = ctypes.POINTER(ctypes.c_uint8)
 
 _SIGS = {
     "orc_validate": (ctypes.c_int, [_C]),
@@ -49,6 +50,15 @@ _SIGS = {
     "orc_decode": (None, [_C, _F, _F, _F, _I, _I, _F, _F, _F, _F, _F, _F]),
     "orc_prefill": (None, [_C, _F, _F, _F, _I, _I, _I, _F, _F, _F, _F, _F, _F]),
     "orc_attention_f64": (None, [_F, _F, _F, _D, _C, _I]),
+    "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+    "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "orc_quantize_row_q4_0": (None, [_F, _SZ, _U8]),
+    "orc_dequantize_row_q4_0": (None, [_U8, _SZ, _F]),
+    "orc_quantize_row_q8_0": (None, [_F, _SZ, _U8]),
+    "orc_dequantize_row_q8_0": (None, [_U8, _SZ, _F]),
+    "orc_vec_dot_q4_0_q8_0_scalar": (ctypes.c_float, [_U8, _U8, _SZ]),
+    "orc_vec_dot_q4_0_q8_0_avx2": (ctypes.c_float, [_U8, _U8, _SZ]),
+    "orc_gemm_q4_0": (None, [_U8, _U8, _F, _I, _I, _I, _I]),
 }
 
 _lib = None
@@ -238,3 +248,87 @@ class OracleModel:
         """Attention of an un-rotated q row at `pos` over the current cache."""
         q_rot = self.rotated_q(q_row, pos)
         return attention(q_rot, self.k_cache(layer), self.v_cache(layer), self.cfg, pos)
+
+
+# ---- quantized projections (src/quant/blocks.rs, src/quant/kernels.rs) ----
+
+QK = 32
+Q4_BYTES = 18
+Q8_BYTES = 34
+
+
+def _u8(a: np.ndarray):
+    assert a.dtype == np.uint8 and a.flags.c_contiguous
+    return a.ctypes.data_as(_U8)
+
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    """half::f16::from_f32(x).to_bits() for every element (uint16)."""
+    x = _f32(x).ravel()
+    L = lib()
+    return np.array([L.orc_f32_to_f16(float(v)) for v in x], dtype=np.uint16)
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    L = lib()
+    return np.array([L.orc_f16_to_f32(int(v)) for v in np.asarray(h).ravel()], dtype=np.float32)
+
+
+def quantize_q4_0(x) -> np.ndarray:
+    """quantize_row_q4_0 (blocks.rs:50-82): [n] f32 -> [n/32][18] bytes."""
+    x = _f32(x).ravel()
+    assert x.size % QK == 0
+    out = np.zeros((x.size // QK, Q4_BYTES), np.uint8)
+    lib().orc_quantize_row_q4_0(_p(x), x.size, _u8(out))
+    return out
+
+
+def dequantize_q4_0(blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1, Q4_BYTES)
+    out = np.zeros(blocks.shape[0] * QK, np.float32)
+    lib().orc_dequantize_row_q4_0(_u8(blocks), blocks.shape[0], _p(out))
+    return out
+
+
+def quantize_q8_0(x) -> np.ndarray:
+    """quantize_row_q8_0 (blocks.rs:102-123): [n] f32 -> [n/32][34] bytes."""
+    x = _f32(x).ravel()
+    assert x.size % QK == 0
+    out = np.zeros((x.size // QK, Q8_BYTES), np.uint8)
+    lib().orc_quantize_row_q8_0(_p(x), x.size, _u8(out))
+    return out
+
+
+def dequantize_q8_0(blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1, Q8_BYTES)
+    out = np.zeros(blocks.shape[0] * QK, np.float32)
+    lib().orc_dequantize_row_q8_0(_u8(blocks), blocks.shape[0], _p(out))
+    return out
+
+
+def vec_dot_q4_0_q8_0(w: np.ndarray, a: np.ndarray, avx2: bool = False) -> float:
+    """vec_dot_q4_0_q8_0_scalar (kernels.rs:145-161) or the AVX2 path (163-212)."""
+    w = np.ascontiguousarray(w, np.uint8).reshape(-1, Q4_BYTES)
+    a = np.ascontiguousarray(a, np.uint8).reshape(-1, Q8_BYTES)
+    assert w.shape[0] == a.shape[0]
+    fn = lib().orc_vec_dot_q4_0_q8_0_avx2 if avx2 else lib().orc_vec_dot_q4_0_q8_0_scalar
+    return float(np.float32(fn(_u8(w), _u8(a), w.shape[0])))
+
+
+def gemm_q4_0(w: np.ndarray, x_q8: np.ndarray, batch: int, rows: int, cols: int,
+              avx2: bool = False) -> np.ndarray:
+    """gemm_q4_0 (kernels.rs:308-394): [batch][rows] f32."""
+    w = np.ascontiguousarray(w, np.uint8).reshape(-1, Q4_BYTES)
+    x_q8 = np.ascontiguousarray(x_q8, np.uint8).reshape(-1, Q8_BYTES)
+    assert cols % QK == 0 and w.shape[0] == rows * cols // QK
+    assert x_q8.shape[0] == batch * cols // QK
+    out = np.zeros((batch, rows), np.float32)
+    lib().orc_gemm_q4_0(_u8(w), _u8(x_q8), _p(out), batch, rows, cols, 1 if avx2 else 0)
+    return out
+
+
+def gemm_q4_0_f32(w: np.ndarray, x, batch: int, rows: int, cols: int,
+                  avx2: bool = False) -> np.ndarray:
+    """gemm_q4_0_arena (kernels.rs:398-415): quantize x [batch][cols] to Q8_0,
+    then gemm_q4_0."""
+    return gemm_q4_0(w, quantize_q8_0(x), batch, rows, cols, avx2)

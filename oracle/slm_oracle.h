@@ -106,6 +106,35 @@ void orc_attention_f64(const float* q, const float* k_cache,
                        const float* v_cache, double* out,
                        const orc_config* cfg, int pos);
 
+/* ---- Quantized projections (src/quant/blocks.rs, src/quant/kernels.rs) ----
+ * Blocks are the reference's byte layouts: BlockQ4_0 = u16 f16 scale + 16
+ * bytes of nibbles (18 B, blocks.rs:11-19), BlockQ8_0 = u16 f16 scale + 32 i8
+ * (34 B, blocks.rs:32-40), scale bytes little-endian. */
+#define ORC_QK 32
+#define ORC_Q4_BYTES 18
+#define ORC_Q8_BYTES 34
+
+/* half::f16::from_f32 / to_f32 (round to nearest even; exact). */
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+
+/* quantize_row_q4_0 (blocks.rs:50-82); n % 32 == 0, dst n/32 blocks. */
+void orc_quantize_row_q4_0(const float* src, size_t n, uint8_t* dst);
+/* dequantize_row_q4_0 (blocks.rs:85-99). */
+void orc_dequantize_row_q4_0(const uint8_t* src, size_t nblocks, float* dst);
+/* quantize_row_q8_0 (blocks.rs:102-123). */
+void orc_quantize_row_q8_0(const float* src, size_t n, uint8_t* dst);
+/* dequantize_row_q8_0 (blocks.rs:126-135). */
+void orc_dequantize_row_q8_0(const uint8_t* src, size_t nblocks, float* dst);
+
+/* vec_dot_q4_0_q8_0_scalar (kernels.rs:145-161). */
+float orc_vec_dot_q4_0_q8_0_scalar(const uint8_t* w, const uint8_t* a, size_t nblocks);
+/* vec_dot_q4_0_q8_0_avx2 (kernels.rs:163-212), restated lane by lane. */
+float orc_vec_dot_q4_0_q8_0_avx2(const uint8_t* w, const uint8_t* a, size_t nblocks);
+/* gemm_q4_0 (kernels.rs:308-394): out[b*rows + r]; avx2 picks the dot. */
+void orc_gemm_q4_0(const uint8_t* w, const uint8_t* x_q8, float* out, int batch, int rows,
+                   int cols, int avx2);
+
 #ifdef __cplusplus
 }
 #endif
