@@ -181,7 +181,9 @@ enum {
     SLM_K_COMBINE = 2, /* merge of the decode split partials */
     SLM_K_PREFILL = 3, /* causal prefill attention */
     SLM_K_ROPE = 4,    /* standalone rope */
-    SLM_K_COUNT = 5
+    SLM_K_QUANT = 5,   /* Q8_0 activation quantization (slm_quant.h) */
+    SLM_K_GEMM = 6,    /* Q4_0 x Q8_0 GEMV / GEMM (slm_quant.h) */
+    SLM_K_COUNT = 7
 };
 typedef struct slm_kernel_stat {
     int64_t launches;

@@ -71,6 +71,14 @@ float orc_f16_to_f32(uint16_t h) {
     return f;
 }
 
+/* Rust's `f as i32`: NaN -> 0, saturating at the i32 range. */
+static inline int32_t rust_f32_as_i32(float f) {
+    if (f != f) return 0;
+    if (f >= 2147483648.0f) return INT32_MAX;
+    if (f <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)f;
+}
+
 static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 static inline void wr16(uint8_t* p, uint16_t v) {
     p[0] = (uint8_t)(v & 0xFF);
@@ -96,8 +104,11 @@ void orc_quantize_row_q4_0(const float* src, size_t n, uint8_t* dst) {
         for (int j = 0; j < ORC_QK / 2; ++j) {
             const float x0 = chunk[j] * id;
             const float x1 = chunk[j + ORC_QK / 2] * id;
-            int q0 = (int)roundf(x0) + 8;
-            int q1 = (int)roundf(x1) + 8;
+            // `x.round() as i32 + 8`, then clamp(0, 15); the add wraps as in a
+            // release build (Cargo.toml's release profile keeps the default
+            // overflow-checks = false), so +inf -> i32::MAX + 8 -> 0
+            int32_t q0 = (int32_t)((uint32_t)rust_f32_as_i32(roundf(x0)) + 8u);
+            int32_t q1 = (int32_t)((uint32_t)rust_f32_as_i32(roundf(x1)) + 8u);
             q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
             q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
             blk[2 + j] = (uint8_t)(q0 | (q1 << 4));
@@ -132,10 +143,12 @@ void orc_quantize_row_q8_0(const float* src, size_t n, uint8_t* dst) {
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
         wr16(blk, orc_f32_to_f16(d));
         for (int j = 0; j < ORC_QK; ++j) {
+            // `.round().clamp(-127.0, 127.0) as i8`: clamp keeps NaN, the cast
+            // sends it to 0
             float v = roundf(chunk[j] * id);
             if (v < -127.0f) v = -127.0f;
             if (v > 127.0f) v = 127.0f;
-            blk[2 + j] = (uint8_t)(int8_t)(int)v;
+            blk[2 + j] = (uint8_t)(int8_t)rust_f32_as_i32(v);
         }
     }
 }

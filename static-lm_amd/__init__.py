@@ -25,6 +25,7 @@ PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libslm_attn.so"
 HEADER_PATH = PKG_DIR.parent / "include" / "slm_attn.h"
 CALIB_HEADER_PATH = PKG_DIR.parent / "include" / "slm_calib.h"
+QUANT_HEADER_PATH = PKG_DIR.parent / "include" / "slm_quant.h"
 
 SLM_OK = 0
 ERRORS = {
@@ -37,11 +38,12 @@ ERRORS = {
     -7: "SLM_ERR_HIP",
     -8: "SLM_ERR_UNSUPPORTED",
     -9: "SLM_ERR_DEVICE",
+    -10: "SLM_ERR_SHAPE",
 }
-ERR_CONFIG, ERR_POS, ERR_BATCH, ERR_LAYER, ERR_ALIAS, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_DEVICE = (
-    -1, -2, -3, -4, -5, -6, -7, -8, -9)
+(ERR_CONFIG, ERR_POS, ERR_BATCH, ERR_LAYER, ERR_ALIAS, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED,
+ ERR_DEVICE, ERR_SHAPE) = (-1, -2, -3, -4, -5, -6, -7, -8, -9, -10)
 
-KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope")
+KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope", "quant", "gemm")
 
 
 class SlmAttnError(RuntimeError):
@@ -124,6 +126,14 @@ SIGNATURES = {
                                           ctypes.POINTER(ctypes.c_double)]),
     "slm_calib_hbm_read": (ctypes.c_int, [_I, ctypes.c_int64, _I,
                                           ctypes.POINTER(ctypes.c_double)]),
+    # slm_quant.h
+    "slm_q4_matrix_create": (ctypes.c_int, [_I, ctypes.c_void_p, _I, _I, ctypes.POINTER(_P)]),
+    "slm_q4_matrix_destroy": (None, [_P]),
+    "slm_q4_matrix_shape": (ctypes.c_int, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "slm_quantize_q8_0_dev": (ctypes.c_int, [_P, _P, ctypes.c_int64, _P]),
+    "slm_gemm_q4_0_dev": (ctypes.c_int, [_P, _P, _P, _I, _P]),
+    "slm_attn_decode_xb_dev": (ctypes.c_int, [_P, _I, _I, _P, _P, _P, _P, _P]),
+    "slm_attn_prefill_xb_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _P, _P, _P]),
 }
 
 _lib = None
@@ -267,6 +277,23 @@ class AttentionContext:
     def kv_append_dev(self, layer, pos0, n, k, v):
         self._check(self.lib.slm_kv_append_dev(self._h, layer, pos0, n, k, v))
 
+    # -- quantized projections (slm_quant.h) -------------------------------------
+    def quantize_q8_0_dev(self, x, n: int, blocks) -> None:
+        self._check(self.lib.slm_quantize_q8_0_dev(self._h, x, n, blocks))
+
+    def gemm_q4_0_dev(self, w: "Q4Matrix", x, batch: int, out) -> None:
+        self._check(self.lib.slm_gemm_q4_0_dev(self._h, w.handle, x, batch, out))
+
+    def decode_xb_dev(self, layer, pos, xb, wq: "Q4Matrix", wk: "Q4Matrix", wv: "Q4Matrix",
+                      out) -> None:
+        self._check(self.lib.slm_attn_decode_xb_dev(self._h, layer, pos, xb, wq.handle,
+                                                    wk.handle, wv.handle, out))
+
+    def prefill_xb_dev(self, layer, start, n, xb, wq: "Q4Matrix", wk: "Q4Matrix",
+                       wv: "Q4Matrix", out) -> None:
+        self._check(self.lib.slm_attn_prefill_xb_dev(self._h, layer, start, n, xb, wq.handle,
+                                                     wk.handle, wv.handle, out))
+
     # -- streams, cache access, timing ------------------------------------------
     def set_stream(self, stream: int | None) -> None:
         self._check(self.lib.slm_attn_set_stream(self._h, stream or None))
@@ -319,11 +346,50 @@ class AttentionContext:
         return ns.value, tile.value
 
 
+class Q4Matrix:
+    """A device-resident Q4_0 weight matrix (slm_q4_matrix_create) from
+    rows*cols/32 BlockQ4_0 of 18 bytes (blocks.rs:11-19), e.g. as a
+    [rows*cols/32, 18] uint8 array."""
+
+    def __init__(self, blocks, rows: int, cols: int, device: int = 0):
+        self.lib = load_library()
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        if blocks.size != rows * (cols // 32) * 18:
+            raise ValueError("blocks must hold rows*cols/32 BlockQ4_0")
+        h = _P()
+        rc = self.lib.slm_q4_matrix_create(device, blocks.ctypes.data, rows, cols, ctypes.byref(h))
+        if rc != SLM_OK:
+            raise SlmAttnError(rc, self.lib.slm_attn_last_error(None).decode())
+        self._h = h
+        self.rows, self.cols = rows, cols
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.slm_q4_matrix_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def header_functions(*headers: os.PathLike | str) -> list[str]:
     """Names of the functions the given headers (default: every include/*.h) declare."""
     import re
 
-    paths = headers or (HEADER_PATH, CALIB_HEADER_PATH)
+    paths = headers or (HEADER_PATH, CALIB_HEADER_PATH, QUANT_HEADER_PATH)
     names = set()
     for h in paths:
         names |= set(re.findall(r"\b(slm_[a-z0-9_]+)\s*\(", Path(h).read_text()))

@@ -22,7 +22,7 @@ HOST_DEMO = PKG_DIR / "slm_host_demo"
 BUILD_DIR = PKG_DIR / "_build"
 
 HIP_SOURCES = ["slm_attn.hip", "rope_append.hip", "attn_decode.hip", "prefill_mfma.hip",
-               "calib.hip"]
+               "quant_gemm.hip", "calib.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [

@@ -1,6 +1,7 @@
 // Host side of the slm_attn C ABI: context, argument checks that mirror the
 // reference's asserts, RoPE tables, device KV region and kernel dispatch.
 #include "../../include/slm_attn.h"
+#include "../../include/slm_quant.h"
 
 #include <math.h>
 #include <stdint.h>
@@ -10,6 +11,16 @@
 #include <vector>
 
 #include "slm_internal.h"
+
+// A Q4_0 weight matrix on one device: nibbles [rows][cols/32][16] and f16
+// scales [rows][cols/32], repacked from 18-byte BlockQ4_0 (blocks.rs:11-19).
+struct slm_q4_matrix {
+    int device = 0;
+    int rows = 0;
+    int cols = 0;
+    uint8_t* qs = nullptr;
+    uint16_t* d = nullptr;
+};
 
 struct slm_attn_ctx {
     slm_attn_config cfg{};
@@ -30,6 +41,13 @@ struct slm_attn_ctx {
     // staging for the host-pointer entry points
     float* stage = nullptr;
     size_t stage_floats = 0;
+    // projections: Q8_0 activations (i8 [blocks][32], f32 scales) and the
+    // q | k | v rows the GEMMs produce for the attention kernels
+    uint32_t* q8_q = nullptr;
+    float* q8_d = nullptr;
+    size_t q8_blocks = 0;
+    float* qkv = nullptr;
+    size_t qkv_floats = 0;
     // kernel timing
     bool profiling = false;
     struct Pending {
@@ -311,6 +329,85 @@ int ensure_stage(slm_attn_ctx* c, size_t floats) {
     return SLM_OK;
 }
 
+// Grows a device buffer (after the stream drained its users).
+template <class T>
+int ensure_buffer(slm_attn_ctx* c, T** buf, size_t* have, size_t want, const char* what) {
+    if (*have >= want) return SLM_OK;
+    if (*buf) {
+        SLM_HIP(c, hipStreamSynchronize(c->stream));
+        SLM_HIP(c, hipFree(*buf));
+        *buf = nullptr;
+        *have = 0;
+    }
+    hipError_t e = hipMalloc(buf, want * sizeof(T));
+    if (e != hipSuccess) return hip_fail(c, e, what);
+    *have = want;
+    return SLM_OK;
+}
+
+int ensure_q8(slm_attn_ctx* c, size_t blocks) {
+    size_t have_q = c->q8_blocks * 8, have_d = c->q8_blocks;
+    int rc = ensure_buffer(c, &c->q8_q, &have_q, blocks * 8, "hipMalloc(q8 activations)");
+    if (rc) return rc;
+    rc = ensure_buffer(c, &c->q8_d, &have_d, blocks, "hipMalloc(q8 scales)");
+    if (rc) return rc;
+    if (blocks > c->q8_blocks) c->q8_blocks = blocks;
+    return SLM_OK;
+}
+
+int check_matrix(slm_attn_ctx* c, const slm_q4_matrix* m, int rows, int cols, const char* name) {
+    if (!m) return fail(c, SLM_ERR_ARG, std::string(name) + " is NULL");
+    if (m->device != c->device)
+        return fail(c, SLM_ERR_DEVICE, std::string(name) + " lives on another device");
+    if ((rows >= 0 && m->rows != rows) || m->cols != cols)
+        return fail(c, SLM_ERR_SHAPE, std::string(name) + " has the wrong shape");
+    return SLM_OK;
+}
+
+slm::Q4Job q4_job(const slm_q4_matrix* m, float* out) {
+    return slm::Q4Job{m->qs, m->d, out, m->rows, m->rows};
+}
+
+// q | k | v of n rows from xb [n][dim]: GEMV (fused quantization) for a few
+// rows, else quantize + MFMA GEMM.  Outputs land in c->qkv.
+int project_qkv(slm_attn_ctx* c, int n, const float* xb, const slm_q4_matrix* wq,
+                const slm_q4_matrix* wk, const slm_q4_matrix* wv, float** q, float** k,
+                float** v) {
+    const slm::Shape& s = c->shape;
+    int rc;
+    if ((rc = check_matrix(c, wq, s.dim, s.dim, "wq")) ||
+        (rc = check_matrix(c, wk, s.kv_dim, s.dim, "wk")) ||
+        (rc = check_matrix(c, wv, s.kv_dim, s.dim, "wv")))
+        return rc;
+    const size_t per_row = (size_t)s.dim + 2 * (size_t)s.kv_dim;
+    if ((rc = ensure_buffer(c, &c->qkv, &c->qkv_floats, (size_t)n * per_row,
+                            "hipMalloc(qkv rows)")))
+        return rc;
+    *q = c->qkv;
+    *k = *q + (size_t)n * s.dim;
+    *v = *k + (size_t)n * s.kv_dim;
+    const slm::Q4Job jobs[3] = {q4_job(wq, *q), q4_job(wk, *k), q4_job(wv, *v)};
+    const int nb = s.dim / 32;
+    if (n <= slm::q4_gemv_max_batch()) {
+        Timed t(c, SLM_K_GEMM);
+        hipError_t e = slm::launch_q4_gemv(jobs, 3, xb, nb, n, c->stream);
+        t.done();
+        return launch_status(c, e, "q4 gemv kernel launch");
+    }
+    const size_t blocks = (size_t)n * nb;
+    if ((rc = ensure_q8(c, blocks))) return rc;
+    {
+        Timed t(c, SLM_K_QUANT);
+        hipError_t e = slm::launch_quantize_q8_soa(xb, (long)blocks, c->q8_q, c->q8_d, c->stream);
+        t.done();
+        if (e != hipSuccess) return hip_fail(c, e, "q8 quantize kernel launch");
+    }
+    Timed t(c, SLM_K_GEMM);
+    hipError_t e = slm::launch_q4_gemm(jobs, 3, c->q8_q, c->q8_d, nb, n, c->stream);
+    t.done();
+    return launch_status(c, e, "q4 gemm kernel launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -424,6 +521,9 @@ void slm_attn_destroy(slm_attn_ctx* c) {
     (void)hipFree(c->part_o);
     (void)hipFree(c->part_ml);
     (void)hipFree(c->stage);
+    (void)hipFree(c->q8_q);
+    (void)hipFree(c->q8_d);
+    (void)hipFree(c->qkv);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }
@@ -674,6 +774,150 @@ int slm_attn_decode_splits(const slm_attn_ctx* c, int32_t seq_len,
     *n_splits = ns;
     *tile = t;
     return SLM_OK;
+}
+
+// ---- slm_quant.h ----------------------------------------------------------
+
+int slm_q4_matrix_create(int32_t device, const void* blocks, int32_t rows, int32_t cols,
+                         slm_q4_matrix** out) {
+    if (!out) return fail(nullptr, SLM_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    if (!blocks) return fail(nullptr, SLM_ERR_ARG, "blocks is NULL");
+    if (rows <= 0 || cols <= 0 || cols % 32 != 0)
+        return fail(nullptr, SLM_ERR_SHAPE, "rows must be positive and cols a positive multiple of 32");
+    if (cols > slm::q4_max_cols())
+        return fail(nullptr, SLM_ERR_UNSUPPORTED, "cols above 16384 is not compiled");
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || device < 0 || device >= ndev)
+        return fail(nullptr, SLM_ERR_DEVICE, "no such HIP device");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess ||
+        strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, SLM_ERR_DEVICE, "this library is built for gfx950 only");
+    const size_t nb = (size_t)cols / 32, nblk = (size_t)rows * nb;
+    std::vector<uint8_t> qs(nblk * 16);
+    std::vector<uint16_t> d(nblk);
+    const uint8_t* src = static_cast<const uint8_t*>(blocks);
+    for (size_t i = 0; i < nblk; ++i) {
+        d[i] = (uint16_t)(src[i * 18] | (src[i * 18 + 1] << 8));
+        memcpy(&qs[i * 16], src + i * 18 + 2, 16);
+    }
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    slm_q4_matrix* m = new slm_q4_matrix();
+    m->device = device;
+    m->rows = rows;
+    m->cols = cols;
+    e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipMalloc(&m->qs, qs.size());
+    if (e == hipSuccess) e = hipMalloc(&m->d, d.size() * 2);
+    if (e == hipSuccess) e = hipMemcpy(m->qs, qs.data(), qs.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(m->d, d.data(), d.size() * 2, hipMemcpyHostToDevice);
+    if (prev >= 0) (void)hipSetDevice(prev);
+    if (e != hipSuccess) {
+        slm_q4_matrix_destroy(m);
+        return hip_fail(nullptr, e, "q4 matrix upload");
+    }
+    *out = m;
+    return SLM_OK;
+}
+
+void slm_q4_matrix_destroy(slm_q4_matrix* m) {
+    if (!m) return;
+    (void)hipFree(m->qs);
+    (void)hipFree(m->d);
+    delete m;
+}
+
+int slm_q4_matrix_shape(const slm_q4_matrix* m, int32_t* rows, int32_t* cols) {
+    if (!m || !rows || !cols) return fail(nullptr, SLM_ERR_ARG, "bad argument");
+    *rows = m->rows;
+    *cols = m->cols;
+    return SLM_OK;
+}
+
+int slm_quantize_q8_0_dev(slm_attn_ctx* c, const float* x, int64_t n, void* blocks) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_dev_ptrs(c, {x}))) return rc;
+    if (!blocks || ((uintptr_t)blocks & 1u)) return fail(c, SLM_ERR_ARG, "blocks must be 2-byte aligned");
+    if (n < 0 || n % 32 != 0) return fail(c, SLM_ERR_SHAPE, "n must be a multiple of 32");
+    if (overlaps(x, (size_t)n * 4, blocks, (size_t)n / 32 * 34))
+        return fail(c, SLM_ERR_ALIAS, "blocks must not overlap x");
+    Timed t(c, SLM_K_QUANT);
+    hipError_t e = slm::launch_quantize_q8_aos(x, (long)(n / 32), static_cast<uint8_t*>(blocks),
+                                               c->stream);
+    t.done();
+    return launch_status(c, e, "q8 quantize kernel launch");
+}
+
+int slm_gemm_q4_0_dev(slm_attn_ctx* c, const slm_q4_matrix* w, const float* x, int32_t batch,
+                      float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_matrix(c, w, -1, w ? w->cols : 0, "w"))) return rc;
+    if (batch < 0) return fail(c, SLM_ERR_SHAPE, "batch must not be negative");
+    if (batch == 0) return SLM_OK;
+    if ((rc = check_dev_ptrs(c, {x, out}))) return rc;
+    if (overlaps(out, (size_t)batch * w->rows * 4, x, (size_t)batch * w->cols * 4))
+        return fail(c, SLM_ERR_ALIAS, "out must not overlap x");
+    const slm::Q4Job job = q4_job(w, out);
+    const int nb = w->cols / 32;
+    if (batch <= slm::q4_gemv_max_batch()) {
+        Timed t(c, SLM_K_GEMM);
+        hipError_t e = slm::launch_q4_gemv(&job, 1, x, nb, batch, c->stream);
+        t.done();
+        return launch_status(c, e, "q4 gemv kernel launch");
+    }
+    const size_t blocks = (size_t)batch * nb;
+    if ((rc = ensure_q8(c, blocks))) return rc;
+    {
+        Timed t(c, SLM_K_QUANT);
+        hipError_t e = slm::launch_quantize_q8_soa(x, (long)blocks, c->q8_q, c->q8_d, c->stream);
+        t.done();
+        if (e != hipSuccess) return hip_fail(c, e, "q8 quantize kernel launch");
+    }
+    Timed t(c, SLM_K_GEMM);
+    hipError_t e = slm::launch_q4_gemm(&job, 1, c->q8_q, c->q8_d, nb, batch, c->stream);
+    t.done();
+    return launch_status(c, e, "q4 gemm kernel launch");
+}
+
+int slm_attn_decode_xb_dev(slm_attn_ctx* c, int32_t layer, int32_t pos, const float* xb,
+                           const slm_q4_matrix* wq, const slm_q4_matrix* wk,
+                           const slm_q4_matrix* wv, float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    const slm::Shape& s = c->shape;
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_pos(c, pos)) ||
+        (rc = check_dev_ptrs(c, {xb, out})) ||
+        (rc = check_out_alias(c, out, s.dim, {{xb, s.dim}}, true)))
+        return rc;
+    float *q, *k, *v;
+    if ((rc = project_qkv(c, 1, xb, wq, wk, wv, &q, &k, &v))) return rc;
+    if (overlaps(out, (size_t)s.dim * 4, c->qkv, c->qkv_floats * 4))
+        return fail(c, SLM_ERR_ALIAS, "out must not overlap the context's buffers");
+    return do_decode(c, layer, pos, q, k, v, out, true);
+}
+
+int slm_attn_prefill_xb_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t n,
+                            const float* xb, const slm_q4_matrix* wq, const slm_q4_matrix* wk,
+                            const slm_q4_matrix* wv, float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    const slm::Shape& s = c->shape;
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_batch(c, start, n)) ||
+        (rc = check_dev_ptrs(c, {xb, out})))
+        return rc;
+    const size_t rows = (size_t)n * s.dim;
+    if ((rc = check_out_alias(c, out, rows, {{xb, rows}}, true))) return rc;
+    float *q, *k, *v;
+    if ((rc = project_qkv(c, n, xb, wq, wk, wv, &q, &k, &v))) return rc;
+    if (overlaps(out, rows * 4, c->qkv, c->qkv_floats * 4))
+        return fail(c, SLM_ERR_ALIAS, "out must not overlap the context's buffers");
+    if ((rc = do_append(c, layer, start, n, k, v))) return rc;
+    return do_attend(c, layer, start, n, q, out, true);
 }
 
 }  // extern "C"

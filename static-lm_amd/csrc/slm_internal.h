@@ -74,4 +74,27 @@ struct PrefillArgs {
 hipError_t launch_prefill_mfma(const Shape& s, const PrefillArgs& a,
                                hipStream_t st);
 
+// Q4_0 x Q8_0 projections (quant_gemm.hip).  A job is one weight matrix:
+// nibbles [rows][nb][16], f16 scales [rows][nb], out[tok * out_stride + row].
+struct Q4Job {
+    const uint8_t* qs;
+    const uint16_t* d;
+    float* out;
+    int rows;
+    int out_stride;
+};
+int q4_max_cols();
+int q4_gemv_max_batch();
+// quantize_row_q8_0 into 34-byte blocks
+hipError_t launch_quantize_q8_aos(const float* x, long nblk, uint8_t* out, hipStream_t st);
+// quantize_row_q8_0 into q [nblk][32] i8 and d [nblk] f32 (the GEMM's input)
+hipError_t launch_quantize_q8_soa(const float* x, long nblk, uint32_t* q, float* d,
+                                  hipStream_t st);
+// batch <= q4_gemv_max_batch(): quantizes x [batch][nb*32] itself
+hipError_t launch_q4_gemv(const Q4Job* jobs, int njobs, const float* x, int nb, int batch,
+                          hipStream_t st);
+// any batch, from pre-quantized activations
+hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
+                          int nb, int batch, hipStream_t st);
+
 }  // namespace slm

@@ -36,6 +36,16 @@ def test_version_and_null_handles():
     # measurement helpers check their arguments before any HIP call
     assert lib.slm_calib_mfma_f32(0, 0, None, None) == P.ERR_ARG
     assert lib.slm_calib_hbm_read(0, 1 << 20, 1, None) == P.ERR_ARG
+    # quantized projections: argument checks before any device work
+    out = P._P()
+    assert lib.slm_q4_matrix_create(0, None, 4, 32, ctypes.byref(out)) == P.ERR_ARG
+    blk = (ctypes.c_uint8 * 18)()
+    assert lib.slm_q4_matrix_create(0, ctypes.addressof(blk), 1, 48, ctypes.byref(out)) == P.ERR_SHAPE
+    assert lib.slm_q4_matrix_create(0, ctypes.addressof(blk), 0, 32, ctypes.byref(out)) == P.ERR_SHAPE
+    assert lib.slm_quantize_q8_0_dev(None, None, 32, None) == P.ERR_ARG
+    assert lib.slm_gemm_q4_0_dev(None, None, None, 1, None) == P.ERR_ARG
+    assert lib.slm_attn_decode_xb_dev(None, 0, 0, None, None, None, None, None) == P.ERR_ARG
+    lib.slm_q4_matrix_destroy(None)  # no-op
 
 
 @pytest.mark.parametrize("dim,heads,kv_heads,msl,layers,theta,why", [
@@ -66,6 +76,6 @@ def test_create_rejects_uncompiled_head_dim():
 
 
 def test_header_declares_error_codes_the_binding_uses():
-    text = P.HEADER_PATH.read_text()
+    text = "".join(h.read_text() for h in (P.HEADER_PATH, P.QUANT_HEADER_PATH))
     for code, name in P.ERRORS.items():
         assert f"#define {name} ({code})" in text
