@@ -31,6 +31,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 REPO = Path(__file__).resolve().parent
 METRIC = "decode attn HBM GB/s @32k ctx; prefill attn TFLOP/s @4k; % of MI355X roofline"
 HBM_PEAK_GBS = 8000.0
@@ -200,6 +202,112 @@ def bench_prefill_4k(torch, P, reps: int) -> dict:
             "profile": prof}
 
 
+def random_q4_blocks(rng, rows: int, cols: int) -> np.ndarray:
+    """Random BlockQ4_0 bytes (random nibbles, f16 scales in [1e-3, 1e-2]):
+    projection timing does not depend on the values."""
+    nblk = rows * (cols // 32)
+    blk = rng.integers(0, 256, (nblk, 18), dtype=np.uint8)
+    blk[:, :2] = rng.uniform(1e-3, 1e-2, nblk).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return blk
+
+
+def bench_block_xb(torch, P, steps: int) -> dict:
+    """The attention block from the attention-RMSNorm output xb: fused Q/K/V
+    GEMV (Q4_0 x Q8_0) + decode at position 32767 over 8 layers, and the
+    4096-row prefill block (Q8_0 quantize + three MFMA GEMMs + append +
+    attention)."""
+    layers, ctx_len = 8, 32768
+    pos = ctx_len - 1
+    rng = np.random.default_rng(17)
+    ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, ctx_len, layers, THETA)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    fill_cache(torch, ctx, layers, ctx_len, ctx_len, 4321)
+    mats = [(P.Q4Matrix(random_q4_blocks(rng, DIM, DIM), DIM, DIM),
+             P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM),
+             P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM)) for _ in range(layers)]
+    xb = torch.randn(layers, DIM, device="cuda")
+    out = torch.empty(layers, DIM, device="cuda")
+
+    def step():
+        for l in range(layers):
+            wq, wk, wv = mats[l]
+            ctx.decode_xb_dev(l, pos, xb[l].data_ptr(), wq, wk, wv, out[l].data_ptr())
+
+    step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ctx.profile(True)
+    for _ in range(steps):
+        step()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    n_g, g_ms = prof["gemm"]
+    gemv_us = g_ms / max(n_g, 1) * 1e3
+    w_bytes = (DIM + 2 * KV_DIM) * (DIM // 32) * 18
+    decode = {
+        "workload": "decode block from xb @32k: fused Q/K/V GEMV (Llama-3-8B Wq/Wk/Wv, Q4_0) "
+                    "+ decode attention, 8 layers",
+        "us_per_layer": ms / layers * 1e3,
+        "gemv_us": gemv_us,
+        "gemv_weight_bytes": w_bytes,
+        "gemv_gbs": w_bytes / (gemv_us / 1e6) / 1e9,
+        "gemv_frac_hbm": w_bytes / (gemv_us / 1e6) / 1e9 / HBM_PEAK_GBS,
+    }
+    for m in mats:
+        for w in m:
+            w.close()
+    ctx.close()
+
+    n, msl = 4096, 8192
+    ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, msl, 1, THETA)
+    ctx.set_stream(stream.cuda_stream)
+    wq = P.Q4Matrix(random_q4_blocks(rng, DIM, DIM), DIM, DIM)
+    wk = P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM)
+    wv = P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM)
+    xs = torch.randn(n, DIM, device="cuda")
+    outs = torch.empty(n, DIM, device="cuda")
+
+    def run():
+        ctx.prefill_xb_dev(0, 0, n, xs.data_ptr(), wq, wk, wv, outs.data_ptr())
+
+    run()
+    torch.cuda.synchronize()
+    reps = 3
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pms = e0.elapsed_time(e1) / reps
+    ctx.profile(True)
+    for _ in range(reps):
+        run()
+    pprof = ctx.profile_read()
+    ctx.profile(False)
+    gemm_ms = pprof["gemm"][1] / max(pprof["gemm"][0], 1)
+    quant_ms = pprof["quant"][1] / max(pprof["quant"][0], 1)
+    macs = n * (DIM + 2 * KV_DIM) * DIM
+    prefill = {
+        "workload": "prefill block from xb, 4096 rows: Q8_0 quantize + Q/K/V MFMA GEMM "
+                    "(Llama-3-8B, Q4_0) + append + causal attention",
+        "ms": pms,
+        "gemm_ms": gemm_ms,
+        "quant_ms": quant_ms,
+        "gemm_int8_tops": 2 * macs / (gemm_ms / 1e3) / 1e12,
+    }
+    for w in (wq, wk, wv):
+        w.close()
+    ctx.close()
+    return {"decode_xb_32k": decode, "prefill_xb_4k": prefill}
+
+
 def bench_decode_131k(torch, P) -> dict:
     pre, steps = 131072, 64
     msl = pre + steps
@@ -293,8 +401,6 @@ def cpu_baseline(budget_s: float) -> dict:
     """The oracle's decode (rope + append + JIT-softmax attention) at position
     32767 of one layer of the same shape, on one host core, repeated until
     the time budget is spent; plus a sample of prefill rows."""
-    import numpy as np
-
     sys.path.insert(0, str(REPO))
     from oracle import py_oracle as orc
 
@@ -411,6 +517,12 @@ def main() -> int:
         log("all configurations")
         wl = bench_workloads(torch, P)
         log(f"decode @131k: {dl['ms_per_step']*1e3:.1f} us/step, {dl['gbs']:.1f} GB/s")
+        log("attention block from xb")
+        bx = bench_block_xb(torch, P, max(3, args.steps // 5))
+        log(f"decode block from xb @32k: {bx['decode_xb_32k']['us_per_layer']:.1f} us/layer, "
+            f"QKV GEMV {bx['decode_xb_32k']['gemv_us']:.2f} us "
+            f"({bx['decode_xb_32k']['gemv_gbs']:.0f} GB/s); prefill block 4k "
+            f"{bx['prefill_xb_4k']['ms']:.3f} ms (GEMM {bx['prefill_xb_4k']['gemm_ms']:.3f} ms)")
         log("calibration")
         cal_mfma = P.calibrate_mfma_f32(iters=20000)
         cal_nt = P.calibrate_hbm_read(4 << 30, nontemporal=True)
@@ -437,6 +549,7 @@ def main() -> int:
                 "workload": "64 decode steps at positions 131072..131135, 1 layer, 1 GiB KV",
             },
             "configs": wl,
+            **bx,
         }
     cpu = None
     if args.cpu_seconds > 0:

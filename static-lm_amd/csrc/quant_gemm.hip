@@ -107,41 +107,57 @@ __global__ __launch_bounds__(256) void quantize_q8_aos_kernel(const float* x, lo
 
 // ---- activations for the MFMA GEMM: q [n][nb][32] i8, d [n][nb] f32 ----
 
-__global__ __launch_bounds__(256) void quantize_q8_soa_kernel(const float* x, long nblk,
-                                                              uint32_t* q, float* d) {
+// d rows are padded to d_stride (nb rounded up to 8) so the GEMM reads eight
+// blocks' scales with two 128-bit loads.
+__global__ __launch_bounds__(256) void quantize_q8_soa_kernel(const float* x, long nblk, int nb,
+                                                              int d_stride, uint32_t* q,
+                                                              float* d) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblk) return;
     const Q8Block b = quantize_q8_block(x + i * 32);
     uint4* o = reinterpret_cast<uint4*>(q + i * 8);
     o[0] = make_uint4(b.q[0], b.q[1], b.q[2], b.q[3]);
     o[1] = make_uint4(b.q[4], b.q[5], b.q[6], b.q[7]);
-    d[i] = h2f(b.dbits);
+    const long tok = i / nb;
+    d[tok * d_stride + (i - tok * nb)] = h2f(b.dbits);
 }
 
-// ---- GEMV: one weight row per wave, blocks lane, lane+64, ... ----
+// ---- GEMV: a workgroup per 16-row tile of one matrix ----
+//
+// Phase 1 quantizes the activation blocks into LDS (four lanes per block;
+// max and integer sums are exact, so any reduction order gives the
+// reference's values).  Phase 2: each wave owns 4 rows, lane l blocks l,
+// l+64, ...; it forms every block term (isum as f32) * (d_w * d_a) and stores
+// it to LDS as [token][row][block].  Phase 3: one lane per (token, row) sums
+// its row's terms in block order, the reference's single f32 accumulator.
 
 struct QMat {
     const uint8_t* qs;   // [rows][nb][16]
-    const uint16_t* d;   // [rows][nb]
+    const uint16_t* d;   // [rows][d_stride], d_stride = nb rounded up to 8
     float* out;          // out[tok * out_stride + row]
     int rows;
     int out_stride;
+    int d_stride;
 };
+
+constexpr int kGemvRowsPerWave = 4;
+constexpr int kGemvRows = 4 * kGemvRowsPerWave;  // rows per workgroup (256 threads)
 
 struct GemvParams {
     QMat m[3];
     int nmat;
+    int tiles[3];    // kGemvRows-row tiles per matrix
     const float* x;  // [batch][nb*32]
     int nb;
     int batch;
 };
 
-constexpr int kGemvWaves = 8;
-constexpr int kGemvRowsPerWave = 2;
-constexpr int kGemvRows = kGemvWaves * kGemvRowsPerWave;  // rows per workgroup
+__device__ __forceinline__ QMat pick(const GemvParams& p, int m) {
+    return m == 0 ? p.m[0] : (m == 1 ? p.m[1] : p.m[2]);
+}
 
 // Block b's integer dot with unsigned nibbles: sum(nib_i * a_i) - 8 * sum(a).
-__device__ __forceinline__ int block_dot(const uint4 w, const uint32_t* a, int asum) {
+__device__ __forceinline__ int block_dot(const uint4 w, const uint32_t (&a)[8], int asum) {
     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
     int s = 0;
 #pragma unroll
@@ -154,98 +170,176 @@ __device__ __forceinline__ int block_dot(const uint4 w, const uint32_t* a, int a
     return s - 8 * asum;
 }
 
+// Four consecutive lanes quantize one block: lane part p holds elements
+// 8p..8p+7; returns them packed (2 dwords), with the block's f16 scale and
+// the sum of its 32 quantized values in every lane of the quad.
+__device__ __forceinline__ void quantize_q8_quad(const float4 f0, const float4 f1, uint2* q,
+                                                 uint16_t* dbits, int* sum) {
+#pragma clang fp contract(off)
+    const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float av = fabsf(v[i]);
+        amax = av > amax ? av : amax;
+    }
+    float o = dpp<0xB1>(amax);  // quad_perm [1,0,3,2]
+    amax = o > amax ? o : amax;
+    o = dpp<0x4E>(amax);        // quad_perm [2,3,0,1]
+    amax = o > amax ? o : amax;
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    int s = 0;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int qv = q8_value(v[i] * id);
+        s += qv;
+        w[i >> 2] |= (uint32_t)(qv & 0xFF) << (8 * (i & 3));
+    }
+    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
+    *q = make_uint2(w[0], w[1]);
+    *dbits = f2h(d);
+    *sum = s;
+}
+
+// Row stride of the block terms in LDS: whole float4s plus 16 bytes, so rows
+// of consecutive lanes start on different banks.
+__host__ __device__ constexpr int gemv_term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
+// Offset (dwords) of the block terms: after q [NT][nb][8], d and sum [NT][nb],
+// rounded up to 16 bytes.
+__host__ __device__ constexpr int gemv_terms_offset(int nt, int nb) {
+    return (nt * nb * 10 + 3) & ~3;
+}
+
 template <int NT, int NBL>
-__global__ __launch_bounds__(64 * kGemvWaves) void gemv_q4_kernel(GemvParams p) {
+__global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
 #pragma clang fp contract(off)
     extern __shared__ __align__(16) uint32_t smem[];
     const int nb = p.nb;
-    uint32_t* s_q = smem;                                   // [NT][nb][8]
+    const int tstride = gemv_term_stride(nb);
+    uint32_t* s_q = smem;                                       // [NT][nb][8]
     float* s_d = reinterpret_cast<float*>(smem + NT * nb * 8);  // [NT][nb]
-    int* s_sum = reinterpret_cast<int*>(s_d + NT * nb);      // [NT][nb]
+    int* s_sum = reinterpret_cast<int*>(s_d + NT * nb);          // [NT][nb]
+    float* s_t = reinterpret_cast<float*>(smem + gemv_terms_offset(NT, nb));  // [NT][16][tstride]
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
 
-    // this wave's rows (over the concatenated matrices), weight loads first
-    int mi[kGemvRowsPerWave], row[kGemvRowsPerWave];
-    bool act[kGemvRowsPerWave];
+    // workgroup -> (matrix, 16-row tile), uniform
+    int tile = blockIdx.x, m = 0;
+    while (m < p.nmat - 1 && tile >= p.tiles[m]) {
+        tile -= p.tiles[m];
+        ++m;
+    }
+    const QMat M = pick(p, m);
+    const int rw = tile * kGemvRows + wave * kGemvRowsPerWave;  // this wave's first row
+
+    // Activation loads of the first kPrePasses quantization passes go out
+    // before the weight loads, so waiting for them does not wait for the
+    // weights (loads complete in issue order) and the quantization overlaps
+    // the weights' trip from HBM.  Quad q of the workgroup takes blocks q,
+    // q+64, ...; addresses are clamped, results past the end are not stored.
+    constexpr int kPrePasses = 2;
+    const int nblk = p.batch * nb;
+    const int quad = threadIdx.x >> 2;
+    const int part = threadIdx.x & 3;
+    float4 xa[kPrePasses][2];
+#pragma unroll
+    for (int k = 0; k < kPrePasses; ++k) {
+        const float* blk = p.x + (long)min(quad + 64 * k, nblk - 1) * 32 + 8 * part;
+        xa[k][0] = ld4(blk);
+        xa[k][1] = ld4(blk + 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
+
+    // Weight loads go out first, all of them before any wait: addresses are
+    // clamped into the matrix instead of guarded (a guarded load with a zero
+    // fallback makes the compiler wait for each load before the next), and
+    // terms of rows or blocks past the end are never read back.
     uint4 wq[kGemvRowsPerWave][NBL];
     uint16_t wd[kGemvRowsPerWave][NBL];
 #pragma unroll
     for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
-        int r = (blockIdx.x * kGemvWaves + wave) * kGemvRowsPerWave + rr;
-        int m = 0;
-        while (m < p.nmat - 1 && r >= p.m[m].rows) {
-            r -= p.m[m].rows;
-            ++m;
-        }
-        mi[rr] = m;
-        row[rr] = r;
-        act[rr] = r < p.m[m].rows;
-        const QMat& M = p.m[m];
+        const int r = min(rw + rr, M.rows - 1);
 #pragma unroll
         for (int j = 0; j < NBL; ++j) {
-            const int b = lane + 64 * j;
-            if (act[rr] && b < nb) {
-                const long blk = (long)r * nb + b;
-                wq[rr][j] = *reinterpret_cast<const uint4*>(M.qs + blk * 16);
-                wd[rr][j] = M.d[blk];
-            } else {
-                wq[rr][j] = make_uint4(0u, 0u, 0u, 0u);
-                wd[rr][j] = 0;
-            }
+            const int b = min(lane + 64 * j, nb - 1);
+            wq[rr][j] = *reinterpret_cast<const uint4*>(M.qs + ((long)r * nb + b) * 16);
+            wd[rr][j] = M.d[(long)r * M.d_stride + b];
         }
     }
 
-    // activations of every token, quantized once per workgroup
-    for (int idx = threadIdx.x; idx < p.batch * nb; idx += 64 * kGemvWaves) {
-        const Q8Block b = quantize_q8_block(p.x + (long)idx * 32);
-        uint4* o = reinterpret_cast<uint4*>(s_q + idx * 8);
-        o[0] = make_uint4(b.q[0], b.q[1], b.q[2], b.q[3]);
-        o[1] = make_uint4(b.q[4], b.q[5], b.q[6], b.q[7]);
-        s_d[idx] = h2f(b.dbits);
-        s_sum[idx] = b.sum;
+    // phase 1: activation blocks of every token
+    for (int k = 0; 64 * k < nblk; ++k) {
+        const int idx = quad + 64 * k;
+        float4 f0, f1;
+        if (k < kPrePasses) {
+            f0 = xa[k < kPrePasses ? k : 0][0];
+            f1 = xa[k < kPrePasses ? k : 0][1];
+        } else {
+            const float* blk = p.x + (long)min(idx, nblk - 1) * 32 + 8 * part;
+            f0 = ld4(blk);
+            f1 = ld4(blk + 4);
+        }
+        uint2 q;
+        uint16_t dbits;
+        int sum;
+        quantize_q8_quad(f0, f1, &q, &dbits, &sum);
+        if (idx < nblk) {  // uniform over the quad
+            *reinterpret_cast<uint2*>(s_q + idx * 8 + 2 * part) = q;
+            if (part == 0) {
+                s_d[idx] = h2f(dbits);
+                s_sum[idx] = sum;
+            }
+        }
     }
     __syncthreads();
 
+    // phase 2: block terms
 #pragma unroll
-    for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
-        if (!act[rr]) continue;  // wave-uniform
-        float t[NBL][NT];
-#pragma unroll
-        for (int j = 0; j < NBL; ++j) {
-            const int b = lane + 64 * j;
-            const float dw = h2f(wd[rr][j]);
-#pragma unroll
-            for (int tok = 0; tok < NT; ++tok) {
-                t[j][tok] = 0.0f;
-                if (b < nb && tok < p.batch) {
-                    const int ai = tok * nb + b;
-                    uint32_t a[8];
-                    const uint4 a0 = *reinterpret_cast<const uint4*>(s_q + ai * 8);
-                    const uint4 a1 = *reinterpret_cast<const uint4*>(s_q + ai * 8 + 4);
-                    a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w;
-                    a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
-                    const int isum = block_dot(wq[rr][j], a, s_sum[ai]);
-                    const float sc = dw * s_d[ai];
-                    t[j][tok] = (float)isum * sc;
-                }
-            }
-        }
-        // the reference's order: one accumulator over blocks 0, 1, 2, ...
-        const QMat& M = p.m[mi[rr]];
+    for (int j = 0; j < NBL; ++j) {
+        const int b = lane + 64 * j;
+        if (b >= nb) break;
 #pragma unroll
         for (int tok = 0; tok < NT; ++tok) {
             if (tok >= p.batch) break;
-            float s = 0.0f;
+            const int ai = tok * nb + b;
+            const uint4 a0 = *reinterpret_cast<const uint4*>(s_q + ai * 8);
+            const uint4 a1 = *reinterpret_cast<const uint4*>(s_q + ai * 8 + 4);
+            const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const float da = s_d[ai];
+            const int asum = s_sum[ai];
 #pragma unroll
-            for (int j = 0; j < NBL; ++j) {
-                const int nl = min(64, nb - 64 * j);
-                const int tv = __float_as_int(t[j][tok]);
-                for (int l = 0; l < nl; ++l)
-                    s = s + __int_as_float(__builtin_amdgcn_readlane(tv, l));
+            for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
+                const int isum = block_dot(wq[rr][j], a, asum);
+                const float sc = h2f(wd[rr][j]) * da;
+                s_t[(tok * kGemvRows + wave * kGemvRowsPerWave + rr) * tstride + b] =
+                    (float)isum * sc;
             }
-            if (lane == 0) M.out[(long)tok * M.out_stride + row[rr]] = s;
+        }
+    }
+    __syncthreads();
+
+    // phase 3: one lane per (token, row), blocks in order
+    if (threadIdx.x < NT * kGemvRows) {
+        const int tok = threadIdx.x / kGemvRows;
+        const int row = threadIdx.x - tok * kGemvRows;
+        const int r = tile * kGemvRows + row;
+        if (tok < p.batch && r < M.rows) {
+            const float* t = s_t + (tok * kGemvRows + row) * tstride;
+            float s = 0.0f;
+            int b = 0;
+            for (; b + 4 <= nb; b += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(t + b);
+                s = s + v.x;
+                s = s + v.y;
+                s = s + v.z;
+                s = s + v.w;
+            }
+            for (; b < nb; ++b) s = s + t[b];
+            M.out[(long)tok * M.out_stride + r] = s;
         }
     }
 }
@@ -264,22 +358,40 @@ struct GemmParams {
     int nmat;
     int tiles[3];          // 64-row tiles per matrix
     const uint32_t* aq;    // [batch][nb][8]
-    const float* ad;       // [batch][nb]
+    const float* ad;       // [batch][d_stride]
     int nb;
+    int d_stride;          // nb rounded up to 8 (weights and activations alike)
     int batch;
 };
 
 constexpr int kGemmTile = 64;
+constexpr int kScaleChunk = 8;  // blocks whose scales one 128-bit load covers
 
 // nibbles 0..15 -> weight - 8 as i8, four per dword
 __device__ __forceinline__ uint32_t nib_to_i8(uint32_t x) {
     return (x + 0x78787878u) ^ 0x80808080u;
 }
 
+// LDS stage of the GEMM: kScaleChunk blocks of the workgroup's 64 weight rows
+// and 64 tokens.  Row strides are padded (36 and 68 dwords) so that the
+// 8-byte fragment reads of a half-wave (16 rows or tokens x 2 lane groups)
+// hit 64 different banks; scales are stored block-major so a lane's four
+// rows are one 8-byte read.
+constexpr int kAStride = 36;  // dwords per weight row: 8 blocks x 16 B + pad
+constexpr int kBStride = 68;  // dwords per token: 8 blocks x 32 B + pad
+struct GemmStage {
+    uint32_t a[kGemmTile * kAStride];
+    uint32_t b[kGemmTile * kBStride];
+    uint16_t dw[kScaleChunk][kGemmTile];
+    float da[kScaleChunk][kGemmTile];
+};
+
 __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    __shared__ __align__(16) GemmStage st[2];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     const int lr = lane & 15;
     const int g = lane >> 4;
 
@@ -292,31 +404,70 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
         rt -= p.tiles[m];
         ++m;
     }
-    const QMat& M = p.m[m];
+    const QMat M = m == 0 ? p.m[0] : (m == 1 ? p.m[1] : p.m[2]);
     const int nb = p.nb;
-    const int r0 = rt * kGemmTile + (wave & 1) * 32;
-    const int t0 = tt * kGemmTile + (wave >> 1) * 32;
+    const int ds = p.d_stride;
+    const int wr0 = rt * kGemmTile;  // workgroup's first row / token
+    const int wt0 = tt * kGemmTile;
 
-    // rows / tokens this lane loads fragments for (clamped in bounds)
-    long wrow[2], atok[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const int r = r0 + 16 * s + lr;
-        wrow[s] = r < M.rows ? r : 0;
-        const int t = t0 + 16 * s + lr;
-        atok[s] = t < p.batch ? t : 0;
-    }
-    // rows whose scales this lane needs: r0 + 16 s + 4 g + j
-    long srow[2][4];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int r = r0 + 16 * s + 4 * g + j;
-            srow[s][j] = r < M.rows ? r : 0;
-        }
-    const int half = (g & 1) * 8;        // byte offset of this lane's 8 nibble bytes
-    const int shift = (g >> 1) * 4;      // low or high nibbles
+    // Stage loads, all 16 bytes wide and coalesced, addresses clamped into
+    // the buffers (rows / tokens / blocks past the end are never used):
+    //   nibbles: thread -> (row tid/4, blocks 2*(tid%4), +1)
+    //   activations: thread -> (token tid/4, blocks 2*(tid%4), +1)
+    //   weight scales: threads 0..63 -> row; activation scales: 64..191.
+    const int lrow = tid >> 2, lsub = tid & 3;
+    const uint8_t* asrc = M.qs + (long)min(wr0 + lrow, M.rows - 1) * nb * 16;
+    const uint32_t* bsrc = p.aq + (long)min(wt0 + lrow, p.batch - 1) * nb * 8;
+    const uint16_t* dwsrc = M.d + (long)min(wr0 + (tid & 63), M.rows - 1) * ds;
+    const int sidx = max(tid - 64, 0);  // threads 64..191 load activation scales
+    const float* dasrc = p.ad + (long)min(wt0 + (sidx >> 1), p.batch - 1) * ds + 4 * (sidx & 1);
+    uint4 ra0, ra1, rb0, rb1, rb2, rb3, rs;
+#define SLM_GEMM_LOAD_STAGE(b0)                                                          \
+    do {                                                                                 \
+        const int blk0 = min((b0) + 2 * lsub, nb - 1);                                   \
+        const int blk1 = min((b0) + 2 * lsub + 1, nb - 1);                               \
+        ra0 = *reinterpret_cast<const uint4*>(asrc + (long)blk0 * 16);                   \
+        ra1 = *reinterpret_cast<const uint4*>(asrc + (long)blk1 * 16);                   \
+        rb0 = *reinterpret_cast<const uint4*>(bsrc + (long)blk0 * 8);                    \
+        rb1 = *reinterpret_cast<const uint4*>(bsrc + (long)blk0 * 8 + 4);                \
+        rb2 = *reinterpret_cast<const uint4*>(bsrc + (long)blk1 * 8);                    \
+        rb3 = *reinterpret_cast<const uint4*>(bsrc + (long)blk1 * 8 + 4);                \
+        if (tid < 64)                                                                    \
+            rs = *reinterpret_cast<const uint4*>(dwsrc + (b0));                          \
+        else if (tid < 192)                                                              \
+            rs = *reinterpret_cast<const uint4*>(dasrc + (b0));                          \
+    } while (0)
+#define SLM_GEMM_STORE_STAGE(S)                                                           \
+    do {                                                                                  \
+        const int kb0 = 2 * lsub;                                                         \
+        *reinterpret_cast<uint4*>(&(S).a[lrow * kAStride + kb0 * 4]) = ra0;               \
+        *reinterpret_cast<uint4*>(&(S).a[lrow * kAStride + kb0 * 4 + 4]) = ra1;           \
+        *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8]) = rb0;               \
+        *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 4]) = rb1;           \
+        *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 8]) = rb2;           \
+        *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 12]) = rb3;          \
+        if (tid < 64) {                                                                   \
+            (S).dw[0][tid] = (uint16_t)(rs.x & 0xFFFF);                                   \
+            (S).dw[1][tid] = (uint16_t)(rs.x >> 16);                                      \
+            (S).dw[2][tid] = (uint16_t)(rs.y & 0xFFFF);                                   \
+            (S).dw[3][tid] = (uint16_t)(rs.y >> 16);                                      \
+            (S).dw[4][tid] = (uint16_t)(rs.z & 0xFFFF);                                   \
+            (S).dw[5][tid] = (uint16_t)(rs.z >> 16);                                      \
+            (S).dw[6][tid] = (uint16_t)(rs.w & 0xFFFF);                                   \
+            (S).dw[7][tid] = (uint16_t)(rs.w >> 16);                                      \
+        } else if (tid < 192) {                                                           \
+            const int t_ = (tid - 64) >> 1, h_ = 4 * ((tid - 64) & 1);                    \
+            (S).da[h_ + 0][t_] = __uint_as_float(rs.x);                                   \
+            (S).da[h_ + 1][t_] = __uint_as_float(rs.y);                                   \
+            (S).da[h_ + 2][t_] = __uint_as_float(rs.z);                                   \
+            (S).da[h_ + 3][t_] = __uint_as_float(rs.w);                                   \
+        }                                                                                 \
+    } while (0)
+
+    // this wave's 32 x 32 quadrant and the lane's fragment coordinates
+    const int qr = (wave & 1) * 32, qt = (wave >> 1) * 32;
+    const int half = (g & 1) * 2;    // dword offset of this lane's 8 nibble bytes
+    const int shift = (g >> 1) * 4;  // low or high nibbles
 
     float acc[2][2][4];
 #pragma unroll
@@ -326,79 +477,101 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[a][b][j] = 0.0f;
 
-    for (int b = 0; b < nb; ++b) {
-        long afrag[2], bfrag[2];
+    SLM_GEMM_LOAD_STAGE(0);
+    SLM_GEMM_STORE_STAGE(st[0]);
+    const int n_stages = (nb + kScaleChunk - 1) / kScaleChunk;
+    for (int sg = 0; sg < n_stages; ++sg) {
+        __syncthreads();  // stage sg is in st[sg & 1]; st[(sg+1) & 1] is free
+        if (sg + 1 < n_stages) SLM_GEMM_LOAD_STAGE((sg + 1) * kScaleChunk);
+        const GemmStage& S = st[sg & 1];
+        const int b0 = sg * kScaleChunk;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const uint2 w = *reinterpret_cast<const uint2*>(M.qs + (wrow[s] * nb + b) * 16 + half);
-            const uint32_t lo = nib_to_i8((w.x >> shift) & 0x0F0F0F0Fu);
-            const uint32_t hi = nib_to_i8((w.y >> shift) & 0x0F0F0F0Fu);
-            afrag[s] = (long)(((uint64_t)hi << 32) | lo);
-            const uint2 a = *reinterpret_cast<const uint2*>(p.aq + (atok[s] * nb + b) * 8 + 2 * g);
-            bfrag[s] = (long)(((uint64_t)a.y << 32) | a.x);
+        for (int kb = 0; kb < kScaleChunk; ++kb) {
+            if (b0 + kb >= nb) break;  // uniform
+            long af[2], bf[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const uint2 w = *reinterpret_cast<const uint2*>(
+                    &S.a[(qr + 16 * s + lr) * kAStride + kb * 4 + half]);
+                const uint32_t lo = nib_to_i8((w.x >> shift) & 0x0F0F0F0Fu);
+                const uint32_t hi = nib_to_i8((w.y >> shift) & 0x0F0F0F0Fu);
+                af[s] = (long)(((uint64_t)hi << 32) | lo);
+                const uint2 x = *reinterpret_cast<const uint2*>(
+                    &S.b[(qt + 16 * s + lr) * kBStride + kb * 8 + 2 * g]);
+                bf[s] = (long)(((uint64_t)x.y << 32) | x.x);
+            }
+            v4i d[2][2];
+#pragma unroll
+            for (int rs2 = 0; rs2 < 2; ++rs2)
+#pragma unroll
+                for (int ts = 0; ts < 2; ++ts)
+                    d[rs2][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[rs2], bf[ts],
+                                                                       v4i{0, 0, 0, 0}, 0, 0, 0);
+            float dw[2][4], da[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const uint2 h = *reinterpret_cast<const uint2*>(&S.dw[kb][qr + 16 * s + 4 * g]);
+                dw[s][0] = h2f((uint16_t)(h.x & 0xFFFF));
+                dw[s][1] = h2f((uint16_t)(h.x >> 16));
+                dw[s][2] = h2f((uint16_t)(h.y & 0xFFFF));
+                dw[s][3] = h2f((uint16_t)(h.y >> 16));
+                da[s] = S.da[kb][qt + 16 * s + lr];
+            }
+#pragma unroll
+            for (int rs2 = 0; rs2 < 2; ++rs2)
+#pragma unroll
+                for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float sc = dw[rs2][j] * da[ts];
+                        acc[rs2][ts][j] = acc[rs2][ts][j] + (float)d[rs2][ts][j] * sc;
+                    }
         }
-        float dw[2][4], da[2];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dw[s][j] = h2f(M.d[srow[s][j] * nb + b]);
-            da[s] = p.ad[atok[s] * nb + b];
-        }
-        v4i d[2][2];
-#pragma unroll
-        for (int rs = 0; rs < 2; ++rs)
-#pragma unroll
-            for (int ts = 0; ts < 2; ++ts)
-                d[rs][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag[rs], bfrag[ts],
-                                                                  v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-        for (int rs = 0; rs < 2; ++rs)
-#pragma unroll
-            for (int ts = 0; ts < 2; ++ts)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float sc = dw[rs][j] * da[ts];
-                    acc[rs][ts][j] = acc[rs][ts][j] + (float)d[rs][ts][j] * sc;
-                }
+        if (sg + 1 < n_stages) SLM_GEMM_STORE_STAGE(st[(sg + 1) & 1]);
     }
 
 #pragma unroll
-    for (int rs = 0; rs < 2; ++rs)
+    for (int rs2 = 0; rs2 < 2; ++rs2)
 #pragma unroll
         for (int ts = 0; ts < 2; ++ts) {
-            const int t = t0 + 16 * ts + lr;
+            const int t = wt0 + qt + 16 * ts + lr;
             if (t >= p.batch) continue;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int r = r0 + 16 * rs + 4 * g + j;
-                if (r < M.rows) M.out[(long)t * M.out_stride + r] = acc[rs][ts][j];
+                const int r = wr0 + qr + 16 * rs2 + 4 * g + j;
+                if (r < M.rows) M.out[(long)t * M.out_stride + r] = acc[rs2][ts][j];
             }
         }
 }
+#undef SLM_GEMM_LOAD_STAGE
+#undef SLM_GEMM_STORE_STAGE
+
+size_t gemv_lds_bytes(int nt, int nb) {
+    return ((size_t)gemv_terms_offset(nt, nb) + (size_t)nt * kGemvRows * gemv_term_stride(nb)) * 4;
+}
 
 template <int NT, int NBL>
-hipError_t launch_gemv_t(const GemvParams& p, int total_rows, hipStream_t st) {
-    const size_t lds = (size_t)NT * p.nb * (8 * 4 + 4 + 4);
+hipError_t launch_gemv_t(const GemvParams& p, int grid, hipStream_t st) {
+    const size_t lds = gemv_lds_bytes(NT, p.nb);
     if (lds > 64 * 1024) {
-        // above the default dynamic-LDS limit (up to 80 KiB of the 160 KiB)
+        // above the default dynamic-LDS limit (at most 106 KiB of the 160 KiB)
         const hipError_t e = hipFuncSetAttribute(
             reinterpret_cast<const void*>(gemv_q4_kernel<NT, NBL>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    const int grid = (total_rows + kGemvRows - 1) / kGemvRows;
-    hipLaunchKernelGGL((gemv_q4_kernel<NT, NBL>), dim3(grid), dim3(64 * kGemvWaves), lds, st, p);
+    hipLaunchKernelGGL((gemv_q4_kernel<NT, NBL>), dim3(grid), dim3(256), lds, st, p);
     return hipGetLastError();
 }
 
 template <int NT>
-hipError_t launch_gemv_nt(const GemvParams& p, int total_rows, hipStream_t st) {
+hipError_t launch_gemv_nt(const GemvParams& p, int grid, hipStream_t st) {
     const int nbl = (p.nb + 63) / 64;
     switch (nbl) {
-        case 1: return launch_gemv_t<NT, 1>(p, total_rows, st);
-        case 2: return launch_gemv_t<NT, 2>(p, total_rows, st);
-        case 3: case 4: return launch_gemv_t<NT, 4>(p, total_rows, st);
-        case 5: case 6: case 7: case 8: return launch_gemv_t<NT, 8>(p, total_rows, st);
+        case 1: return launch_gemv_t<NT, 1>(p, grid, st);
+        case 2: return launch_gemv_t<NT, 2>(p, grid, st);
+        case 3: case 4: return launch_gemv_t<NT, 4>(p, grid, st);
+        case 5: case 6: case 7: case 8: return launch_gemv_t<NT, 8>(p, grid, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -406,7 +579,6 @@ hipError_t launch_gemv_nt(const GemvParams& p, int total_rows, hipStream_t st) {
 }  // namespace
 
 int q4_max_cols() { return 64 * 8 * 32; }
-int q4_gemv_max_batch() { return 4; }
 
 hipError_t launch_quantize_q8_aos(const float* x, long nblk, uint8_t* out, hipStream_t st) {
     if (nblk <= 0) return hipSuccess;
@@ -415,28 +587,37 @@ hipError_t launch_quantize_q8_aos(const float* x, long nblk, uint8_t* out, hipSt
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_q8_soa(const float* x, long nblk, uint32_t* q, float* d,
+int q4_scale_stride(int nb) { return (nb + kScaleChunk - 1) / kScaleChunk * kScaleChunk; }
+
+hipError_t launch_quantize_q8_soa(const float* x, long ntok, int nb, uint32_t* q, float* d,
                                   hipStream_t st) {
+    const long nblk = ntok * nb;
     if (nblk <= 0) return hipSuccess;
     hipLaunchKernelGGL(quantize_q8_soa_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256),
-                       0, st, x, nblk, q, d);
+                       0, st, x, nblk, nb, q4_scale_stride(nb), q, d);
     return hipGetLastError();
+}
+
+bool q4_gemv_takes(int nb, int batch) {
+    return batch >= 1 && (batch == 1 || (batch <= 4 && nb <= 256));
 }
 
 hipError_t launch_q4_gemv(const Q4Job* jobs, int njobs, const float* x, int nb, int batch,
                           hipStream_t st) {
-    if (njobs < 1 || njobs > 3 || batch < 1 || batch > q4_gemv_max_batch()) return hipErrorInvalidValue;
+    if (njobs < 1 || njobs > 3 || !q4_gemv_takes(nb, batch)) return hipErrorInvalidValue;
     GemvParams p{};
-    int total = 0;
+    int grid = 0;
     for (int i = 0; i < njobs; ++i) {
-        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].rows, jobs[i].out_stride};
-        total += jobs[i].rows;
+        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].rows, jobs[i].out_stride,
+                      q4_scale_stride(nb)};
+        p.tiles[i] = (jobs[i].rows + kGemvRows - 1) / kGemvRows;
+        grid += p.tiles[i];
     }
     p.nmat = njobs;
     p.x = x;
     p.nb = nb;
     p.batch = batch;
-    return batch == 1 ? launch_gemv_nt<1>(p, total, st) : launch_gemv_nt<4>(p, total, st);
+    return batch == 1 ? launch_gemv_nt<1>(p, grid, st) : launch_gemv_nt<4>(p, grid, st);
 }
 
 hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
@@ -445,7 +626,8 @@ hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, cons
     GemmParams p{};
     long tiles = 0;
     for (int i = 0; i < njobs; ++i) {
-        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].rows, jobs[i].out_stride};
+        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].rows, jobs[i].out_stride,
+                      q4_scale_stride(nb)};
         p.tiles[i] = (jobs[i].rows + kGemmTile - 1) / kGemmTile;
         tiles += p.tiles[i];
     }
@@ -453,6 +635,7 @@ hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, cons
     p.aq = aq;
     p.ad = ad;
     p.nb = nb;
+    p.d_stride = q4_scale_stride(nb);
     p.batch = batch;
     const long n_tt = (batch + kGemmTile - 1) / kGemmTile;
     if (tiles * n_tt > 0x7FFFFFFF) return hipErrorInvalidValue;

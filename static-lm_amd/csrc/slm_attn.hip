@@ -13,7 +13,8 @@
 #include "slm_internal.h"
 
 // A Q4_0 weight matrix on one device: nibbles [rows][cols/32][16] and f16
-// scales [rows][cols/32], repacked from 18-byte BlockQ4_0 (blocks.rs:11-19).
+// scales [rows][cols/32 rounded up to 8], repacked from 18-byte BlockQ4_0
+// (blocks.rs:11-19).
 struct slm_q4_matrix {
     int device = 0;
     int rows = 0;
@@ -345,7 +346,10 @@ int ensure_buffer(slm_attn_ctx* c, T** buf, size_t* have, size_t want, const cha
     return SLM_OK;
 }
 
-int ensure_q8(slm_attn_ctx* c, size_t blocks) {
+// Q8_0 activations of n rows of nb blocks: i8 [n][nb][32] and f32 scales
+// [n][q4_scale_stride(nb)].
+int ensure_q8(slm_attn_ctx* c, size_t n, int nb) {
+    const size_t blocks = n * (size_t)slm::q4_scale_stride(nb);  // covers both
     size_t have_q = c->q8_blocks * 8, have_d = c->q8_blocks;
     int rc = ensure_buffer(c, &c->q8_q, &have_q, blocks * 8, "hipMalloc(q8 activations)");
     if (rc) return rc;
@@ -388,17 +392,16 @@ int project_qkv(slm_attn_ctx* c, int n, const float* xb, const slm_q4_matrix* wq
     *v = *k + (size_t)n * s.kv_dim;
     const slm::Q4Job jobs[3] = {q4_job(wq, *q), q4_job(wk, *k), q4_job(wv, *v)};
     const int nb = s.dim / 32;
-    if (n <= slm::q4_gemv_max_batch()) {
+    if (slm::q4_gemv_takes(nb, n)) {
         Timed t(c, SLM_K_GEMM);
         hipError_t e = slm::launch_q4_gemv(jobs, 3, xb, nb, n, c->stream);
         t.done();
         return launch_status(c, e, "q4 gemv kernel launch");
     }
-    const size_t blocks = (size_t)n * nb;
-    if ((rc = ensure_q8(c, blocks))) return rc;
+    if ((rc = ensure_q8(c, (size_t)n, nb))) return rc;
     {
         Timed t(c, SLM_K_QUANT);
-        hipError_t e = slm::launch_quantize_q8_soa(xb, (long)blocks, c->q8_q, c->q8_d, c->stream);
+        hipError_t e = slm::launch_quantize_q8_soa(xb, n, nb, c->q8_q, c->q8_d, c->stream);
         t.done();
         if (e != hipSuccess) return hip_fail(c, e, "q8 quantize kernel launch");
     }
@@ -795,12 +798,16 @@ int slm_q4_matrix_create(int32_t device, const void* blocks, int32_t rows, int32
     if (hipGetDeviceProperties(&prop, device) != hipSuccess ||
         strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(nullptr, SLM_ERR_DEVICE, "this library is built for gfx950 only");
+    // nibbles [rows][nb][16]; f16 scales [rows][ds], ds = nb rounded up to 8
+    // (zero padded) so kernels read eight scales with one 128-bit load
     const size_t nb = (size_t)cols / 32, nblk = (size_t)rows * nb;
+    const size_t ds = (size_t)slm::q4_scale_stride((int)nb);
     std::vector<uint8_t> qs(nblk * 16);
-    std::vector<uint16_t> d(nblk);
+    std::vector<uint16_t> d((size_t)rows * ds, 0);
     const uint8_t* src = static_cast<const uint8_t*>(blocks);
     for (size_t i = 0; i < nblk; ++i) {
-        d[i] = (uint16_t)(src[i * 18] | (src[i * 18 + 1] << 8));
+        const size_t r = i / nb, b = i - r * nb;
+        d[r * ds + b] = (uint16_t)(src[i * 18] | (src[i * 18 + 1] << 8));
         memcpy(&qs[i * 16], src + i * 18 + 2, 16);
     }
     int prev = 0;
@@ -864,17 +871,16 @@ int slm_gemm_q4_0_dev(slm_attn_ctx* c, const slm_q4_matrix* w, const float* x, i
         return fail(c, SLM_ERR_ALIAS, "out must not overlap x");
     const slm::Q4Job job = q4_job(w, out);
     const int nb = w->cols / 32;
-    if (batch <= slm::q4_gemv_max_batch()) {
+    if (slm::q4_gemv_takes(nb, batch)) {
         Timed t(c, SLM_K_GEMM);
         hipError_t e = slm::launch_q4_gemv(&job, 1, x, nb, batch, c->stream);
         t.done();
         return launch_status(c, e, "q4 gemv kernel launch");
     }
-    const size_t blocks = (size_t)batch * nb;
-    if ((rc = ensure_q8(c, blocks))) return rc;
+    if ((rc = ensure_q8(c, (size_t)batch, nb))) return rc;
     {
         Timed t(c, SLM_K_QUANT);
-        hipError_t e = slm::launch_quantize_q8_soa(x, (long)blocks, c->q8_q, c->q8_d, c->stream);
+        hipError_t e = slm::launch_quantize_q8_soa(x, batch, nb, c->q8_q, c->q8_d, c->stream);
         t.done();
         if (e != hipSuccess) return hip_fail(c, e, "q8 quantize kernel launch");
     }

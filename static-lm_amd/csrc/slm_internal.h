@@ -75,7 +75,8 @@ hipError_t launch_prefill_mfma(const Shape& s, const PrefillArgs& a,
                                hipStream_t st);
 
 // Q4_0 x Q8_0 projections (quant_gemm.hip).  A job is one weight matrix:
-// nibbles [rows][nb][16], f16 scales [rows][nb], out[tok * out_stride + row].
+// nibbles [rows][nb][16], f16 scales [rows][q4_scale_stride(nb)],
+// out[tok * out_stride + row].
 struct Q4Job {
     const uint8_t* qs;
     const uint16_t* d;
@@ -84,13 +85,18 @@ struct Q4Job {
     int out_stride;
 };
 int q4_max_cols();
-int q4_gemv_max_batch();
+// scale row length: nb rounded up to 8 (the GEMM reads 8 scales per load)
+int q4_scale_stride(int nb);
+// whether the GEMV takes a batch of this size (batch 1 always; up to 4 rows of
+// at most 256 blocks)
+bool q4_gemv_takes(int nb, int batch);
 // quantize_row_q8_0 into 34-byte blocks
 hipError_t launch_quantize_q8_aos(const float* x, long nblk, uint8_t* out, hipStream_t st);
-// quantize_row_q8_0 into q [nblk][32] i8 and d [nblk] f32 (the GEMM's input)
-hipError_t launch_quantize_q8_soa(const float* x, long nblk, uint32_t* q, float* d,
+// quantize_row_q8_0 of ntok rows of nb blocks into q [ntok][nb][32] i8 and
+// d [ntok][q4_scale_stride(nb)] f32 (the GEMM's input)
+hipError_t launch_quantize_q8_soa(const float* x, long ntok, int nb, uint32_t* q, float* d,
                                   hipStream_t st);
-// batch <= q4_gemv_max_batch(): quantizes x [batch][nb*32] itself
+// a batch q4_gemv_takes(): quantizes x [batch][nb*32] itself
 hipError_t launch_q4_gemv(const Q4Job* jobs, int njobs, const float* x, int nb, int batch,
                           hipStream_t st);
 // any batch, from pre-quantized activations
