@@ -461,6 +461,9 @@ def main() -> int:
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 4096-row prefill (a short program for counter passes); "
                          "prints its own JSON line, not the headline one")
+    ap.add_argument("--xb-only", action="store_true",
+                    help="only the attention block from xb (Q/K/V projections + attention); "
+                         "prints its own JSON line, not the headline one")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB: a plain "
                          "copy kernel of known size that scales rocprofv3 byte counters")
@@ -495,6 +498,11 @@ def main() -> int:
         log(f"copy calibration: {args.copy_calibration_mib} MiB read + "
             f"{args.copy_calibration_mib} MiB written")
         del src, dst
+
+    if args.xb_only:
+        bx = bench_block_xb(torch, P, max(3, args.steps // 5))
+        print(json.dumps(bx))
+        return 0
 
     if args.prefill_only:
         pf = bench_prefill_4k(torch, P, reps=max(3, args.steps // 10))

@@ -36,14 +36,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 
-// One Q8_0 block from 32 floats: packed i8 (little-endian bytes), the f16
-// scale bits, and the sum of the 32 quantized values.
-struct Q8Block {
-    uint32_t q[8];
-    uint16_t dbits;
-    int sum;
-};
-
 // `(x * id).round().clamp(-127.0, 127.0) as i8`: round half away from zero,
 // clamp keeps NaN, the cast sends NaN to 0.
 __device__ __forceinline__ int q8_value(float v) {
@@ -52,74 +44,82 @@ __device__ __forceinline__ int q8_value(float v) {
     return r != r ? 0 : (int)r;
 }
 
-__device__ __forceinline__ Q8Block quantize_q8_block(const float* x) {
+// Four consecutive lanes quantize one block: lane part p holds elements
+// 8p..8p+7; returns them packed (2 dwords), with the block's f16 scale and
+// the sum of its 32 quantized values in every lane of the quad.
+__device__ __forceinline__ void quantize_q8_quad(const float4 f0, const float4 f1, uint2* q,
+                                                 uint16_t* dbits, int* sum) {
 #pragma clang fp contract(off)
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 f = ld4(x + 4 * i);
-        v[4 * i + 0] = f.x;
-        v[4 * i + 1] = f.y;
-        v[4 * i + 2] = f.z;
-        v[4 * i + 3] = f.w;
-    }
+    const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 8; ++i) {
         const float av = fabsf(v[i]);
         amax = av > amax ? av : amax;
     }
+    float o = dpp<0xB1>(amax);  // quad_perm [1,0,3,2]
+    amax = o > amax ? o : amax;
+    o = dpp<0x4E>(amax);        // quad_perm [2,3,0,1]
+    amax = o > amax ? o : amax;
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    Q8Block b;
-    b.dbits = f2h(d);
-    b.sum = 0;
+    int s = 0;
+    uint32_t w[2] = {0u, 0u};
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int q = q8_value(v[4 * k + e] * id);
-            b.sum += q;
-            w |= (uint32_t)(q & 0xFF) << (8 * e);
-        }
-        b.q[k] = w;
+    for (int i = 0; i < 8; ++i) {
+        const int qv = q8_value(v[i] * id);
+        s += qv;
+        w[i >> 2] |= (uint32_t)(qv & 0xFF) << (8 * (i & 3));
     }
-    return b;
+    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
+    *q = make_uint2(w[0], w[1]);
+    *dbits = f2h(d);
+    *sum = s;
 }
 
 // ---- standalone quantize_row_q8_0: 34-byte BlockQ8_0 output ----
+// Four lanes per block (coalesced 32-byte reads per lane).
 
 __global__ __launch_bounds__(256) void quantize_q8_aos_kernel(const float* x, long nblk,
                                                               uint8_t* out) {
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nblk) return;
-    const Q8Block b = quantize_q8_block(x + i * 32);
-    // 34-byte blocks are 2-byte aligned: 17 little-endian u16 stores
+    const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 2;
+    const int part = threadIdx.x & 3;
+    if (i >= nblk) return;  // uniform over the quad
+    const float* blk = x + i * 32 + 8 * part;
+    uint2 q;
+    uint16_t dbits;
+    int sum;
+    quantize_q8_quad(ld4(blk), ld4(blk + 4), &q, &dbits, &sum);
+    // 34-byte blocks are 2-byte aligned: little-endian u16 stores
     uint16_t* o = reinterpret_cast<uint16_t*>(out + i * 34);
-    o[0] = b.dbits;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        o[1 + 2 * k] = (uint16_t)(b.q[k] & 0xFFFF);
-        o[2 + 2 * k] = (uint16_t)(b.q[k] >> 16);
-    }
+    if (part == 0) o[0] = dbits;
+    o[1 + 4 * part + 0] = (uint16_t)(q.x & 0xFFFF);
+    o[1 + 4 * part + 1] = (uint16_t)(q.x >> 16);
+    o[1 + 4 * part + 2] = (uint16_t)(q.y & 0xFFFF);
+    o[1 + 4 * part + 3] = (uint16_t)(q.y >> 16);
 }
 
-// ---- activations for the MFMA GEMM: q [n][nb][32] i8, d [n][nb] f32 ----
-
+// ---- activations for the MFMA GEMM: q [n][nb][32] i8, d [n][d_stride] f32 ----
 // d rows are padded to d_stride (nb rounded up to 8) so the GEMM reads eight
 // blocks' scales with two 128-bit loads.
+
 __global__ __launch_bounds__(256) void quantize_q8_soa_kernel(const float* x, long nblk, int nb,
                                                               int d_stride, uint32_t* q,
                                                               float* d) {
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nblk) return;
-    const Q8Block b = quantize_q8_block(x + i * 32);
-    uint4* o = reinterpret_cast<uint4*>(q + i * 8);
-    o[0] = make_uint4(b.q[0], b.q[1], b.q[2], b.q[3]);
-    o[1] = make_uint4(b.q[4], b.q[5], b.q[6], b.q[7]);
-    const long tok = i / nb;
-    d[tok * d_stride + (i - tok * nb)] = h2f(b.dbits);
+    const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 2;
+    const int part = threadIdx.x & 3;
+    if (i >= nblk) return;  // uniform over the quad
+    const float* blk = x + i * 32 + 8 * part;
+    uint2 qv;
+    uint16_t dbits;
+    int sum;
+    quantize_q8_quad(ld4(blk), ld4(blk + 4), &qv, &dbits, &sum);
+    *reinterpret_cast<uint2*>(q + i * 8 + 2 * part) = qv;
+    if (part == 0) {
+        const long tok = i / nb;
+        d[tok * d_stride + (i - tok * nb)] = h2f(dbits);
+    }
 }
 
 // ---- GEMV: a workgroup per 16-row tile of one matrix ----
@@ -170,39 +170,6 @@ __device__ __forceinline__ int block_dot(const uint4 w, const uint32_t (&a)[8], 
     return s - 8 * asum;
 }
 
-// Four consecutive lanes quantize one block: lane part p holds elements
-// 8p..8p+7; returns them packed (2 dwords), with the block's f16 scale and
-// the sum of its 32 quantized values in every lane of the quad.
-__device__ __forceinline__ void quantize_q8_quad(const float4 f0, const float4 f1, uint2* q,
-                                                 uint16_t* dbits, int* sum) {
-#pragma clang fp contract(off)
-    const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float av = fabsf(v[i]);
-        amax = av > amax ? av : amax;
-    }
-    float o = dpp<0xB1>(amax);  // quad_perm [1,0,3,2]
-    amax = o > amax ? o : amax;
-    o = dpp<0x4E>(amax);        // quad_perm [2,3,0,1]
-    amax = o > amax ? o : amax;
-    const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    int s = 0;
-    uint32_t w[2] = {0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int qv = q8_value(v[i] * id);
-        s += qv;
-        w[i >> 2] |= (uint32_t)(qv & 0xFF) << (8 * (i & 3));
-    }
-    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
-    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
-    *q = make_uint2(w[0], w[1]);
-    *dbits = f2h(d);
-    *sum = s;
-}
 
 // Row stride of the block terms in LDS: whole float4s plus 16 bytes, so rows
 // of consecutive lanes start on different banks.
@@ -582,7 +549,7 @@ int q4_max_cols() { return 64 * 8 * 32; }
 
 hipError_t launch_quantize_q8_aos(const float* x, long nblk, uint8_t* out, hipStream_t st) {
     if (nblk <= 0) return hipSuccess;
-    hipLaunchKernelGGL(quantize_q8_aos_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256),
+    hipLaunchKernelGGL(quantize_q8_aos_kernel, dim3((unsigned)((nblk + 63) / 64)), dim3(256),
                        0, st, x, nblk, out);
     return hipGetLastError();
 }
@@ -593,7 +560,7 @@ hipError_t launch_quantize_q8_soa(const float* x, long ntok, int nb, uint32_t* q
                                   hipStream_t st) {
     const long nblk = ntok * nb;
     if (nblk <= 0) return hipSuccess;
-    hipLaunchKernelGGL(quantize_q8_soa_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256),
+    hipLaunchKernelGGL(quantize_q8_soa_kernel, dim3((unsigned)((nblk + 63) / 64)), dim3(256),
                        0, st, x, nblk, nb, q4_scale_stride(nb), q, d);
     return hipGetLastError();
 }
