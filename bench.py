@@ -211,11 +211,34 @@ def random_q4_blocks(rng, rows: int, cols: int) -> np.ndarray:
     return blk
 
 
+def _ms_per_call(torch, stream, fn, reps: int) -> float:
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _profiled(ctx, fn, reps: int) -> dict:
+    ctx.profile(True)
+    for _ in range(reps):
+        fn()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    return prof
+
+
 def bench_block_xb(torch, P, steps: int) -> dict:
-    """The attention block from the attention-RMSNorm output xb: fused Q/K/V
-    GEMV (Q4_0 x Q8_0) + decode at position 32767 over 8 layers, and the
-    4096-row prefill block (Q8_0 quantize + three MFMA GEMMs + append +
-    attention)."""
+    """The attention half of the transformer block from the attention-RMSNorm
+    output xb to the residual stream: fused Q/K/V GEMV (Q4_0 x Q8_0) + decode
+    at position 32767 + Wo GEMV with the residual add, over 8 layers; the
+    projections with residual alone at the Wo and w_down shapes; and the
+    4096-row prefill block (Q8_0 quantize + Q/K/V MFMA GEMM + append +
+    attention + Wo GEMM with the residual add)."""
     layers, ctx_len = 8, 32768
     pos = ctx_len - 1
     rng = np.random.default_rng(17)
@@ -225,44 +248,70 @@ def bench_block_xb(torch, P, steps: int) -> dict:
     fill_cache(torch, ctx, layers, ctx_len, ctx_len, 4321)
     mats = [(P.Q4Matrix(random_q4_blocks(rng, DIM, DIM), DIM, DIM),
              P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM),
-             P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM)) for _ in range(layers)]
+             P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM),
+             P.Q4Matrix(random_q4_blocks(rng, DIM, DIM), DIM, DIM)) for _ in range(layers)]
     xb = torch.randn(layers, DIM, device="cuda")
+    x = torch.randn(layers, DIM, device="cuda")
     out = torch.empty(layers, DIM, device="cuda")
 
-    def step():
+    def qkv_step():
         for l in range(layers):
-            wq, wk, wv = mats[l]
+            wq, wk, wv, _ = mats[l]
             ctx.decode_xb_dev(l, pos, xb[l].data_ptr(), wq, wk, wv, out[l].data_ptr())
 
-    step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
-    ctx.profile(True)
-    for _ in range(steps):
-        step()
-    prof = ctx.profile_read()
-    ctx.profile(False)
+    def block_step():
+        for l in range(layers):
+            wq, wk, wv, wo = mats[l]
+            ctx.decode_wo_dev(l, pos, xb[l].data_ptr(), wq, wk, wv, wo, x[l].data_ptr(),
+                              out[l].data_ptr())
+
+    qkv_ms = _ms_per_call(torch, stream, qkv_step, steps)
+    prof = _profiled(ctx, qkv_step, steps)
     n_g, g_ms = prof["gemm"]
     gemv_us = g_ms / max(n_g, 1) * 1e3
+    block_ms = _ms_per_call(torch, stream, block_step, steps)
+    bprof = _profiled(ctx, block_step, steps)
+    wo_us = (bprof["gemm"][1] - g_ms) / max(bprof["gemm"][0] - n_g, 1) * 1e3
     w_bytes = (DIM + 2 * KV_DIM) * (DIM // 32) * 18
+    wo_bytes = DIM * (DIM // 32) * 18
     decode = {
-        "workload": "decode block from xb @32k: fused Q/K/V GEMV (Llama-3-8B Wq/Wk/Wv, Q4_0) "
-                    "+ decode attention, 8 layers",
-        "us_per_layer": ms / layers * 1e3,
+        "workload": "decode attention block from xb @32k, 8 layers: fused Q/K/V GEMV "
+                    "(Llama-3-8B Wq/Wk/Wv, Q4_0) + decode attention + Wo GEMV with residual",
+        "us_per_layer": block_ms / layers * 1e3,
+        "us_per_layer_without_wo": qkv_ms / layers * 1e3,
         "gemv_us": gemv_us,
         "gemv_weight_bytes": w_bytes,
         "gemv_gbs": w_bytes / (gemv_us / 1e6) / 1e9,
         "gemv_frac_hbm": w_bytes / (gemv_us / 1e6) / 1e9 / HBM_PEAK_GBS,
+        "wo_gemv_us": wo_us,
+        "wo_gemv_gbs": wo_bytes / (wo_us / 1e6) / 1e9,
     }
     for m in mats:
         for w in m:
             w.close()
+
+    # projection + residual alone: Wo (dim x dim) and w_down (dim x 14336),
+    # 8 distinct matrices in turn so the weights stream from HBM
+    hidden = 14336
+    proj = {}
+    for name, cols in (("wo", DIM), ("w_down", hidden)):
+        ws = [P.Q4Matrix(random_q4_blocks(rng, DIM, cols), DIM, cols) for _ in range(layers)]
+        xin = torch.randn(cols, device="cuda")
+        res = torch.randn(DIM, device="cuda")
+
+        def run_proj():
+            for w in ws:
+                ctx.gemm_q4_0_residual_dev(w, xin.data_ptr(), 1, res.data_ptr(), res.data_ptr())
+
+        pp = _profiled(ctx, run_proj, steps)
+        us = pp["gemm"][1] / max(pp["gemm"][0], 1) * 1e3
+        nbytes = DIM * (cols // 32) * 18
+        proj[name] = {"rows": DIM, "cols": cols, "us": us, "weight_bytes": nbytes,
+                      "gbs": nbytes / (us / 1e6) / 1e9,
+                      "frac_hbm": nbytes / (us / 1e6) / 1e9 / HBM_PEAK_GBS}
+        for w in ws:
+            w.close()
+    decode["residual_gemv"] = proj
     ctx.close()
 
     n, msl = 4096, 8192
@@ -271,38 +320,40 @@ def bench_block_xb(torch, P, steps: int) -> dict:
     wq = P.Q4Matrix(random_q4_blocks(rng, DIM, DIM), DIM, DIM)
     wk = P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM)
     wv = P.Q4Matrix(random_q4_blocks(rng, KV_DIM, DIM), KV_DIM, DIM)
+    wo = P.Q4Matrix(random_q4_blocks(rng, DIM, DIM), DIM, DIM)
     xs = torch.randn(n, DIM, device="cuda")
+    xres = torch.randn(n, DIM, device="cuda")
     outs = torch.empty(n, DIM, device="cuda")
 
-    def run():
+    def run_qkv():
         ctx.prefill_xb_dev(0, 0, n, xs.data_ptr(), wq, wk, wv, outs.data_ptr())
 
-    run()
-    torch.cuda.synchronize()
+    def run_block():
+        ctx.prefill_wo_dev(0, 0, n, xs.data_ptr(), wq, wk, wv, wo, xres.data_ptr(),
+                           outs.data_ptr())
+
     reps = 3
-    e0.record(stream)
-    for _ in range(reps):
-        run()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    pms = e0.elapsed_time(e1) / reps
-    ctx.profile(True)
-    for _ in range(reps):
-        run()
-    pprof = ctx.profile_read()
-    ctx.profile(False)
+    qkv_ms = _ms_per_call(torch, stream, run_qkv, reps)
+    pprof = _profiled(ctx, run_qkv, reps)
     gemm_ms = pprof["gemm"][1] / max(pprof["gemm"][0], 1)
     quant_ms = pprof["quant"][1] / max(pprof["quant"][0], 1)
+    block_ms = _ms_per_call(torch, stream, run_block, reps)
+    bprof = _profiled(ctx, run_block, reps)
+    wo_ms = (bprof["gemm"][1] - pprof["gemm"][1]) / max(bprof["gemm"][0] - pprof["gemm"][0], 1)
     macs = n * (DIM + 2 * KV_DIM) * DIM
     prefill = {
-        "workload": "prefill block from xb, 4096 rows: Q8_0 quantize + Q/K/V MFMA GEMM "
-                    "(Llama-3-8B, Q4_0) + append + causal attention",
-        "ms": pms,
+        "workload": "prefill attention block from xb, 4096 rows: Q8_0 quantize + Q/K/V MFMA "
+                    "GEMM (Llama-3-8B, Q4_0) + append + causal attention + Q8_0 quantize + "
+                    "Wo MFMA GEMM with residual",
+        "ms": block_ms,
+        "ms_without_wo": qkv_ms,
         "gemm_ms": gemm_ms,
         "quant_ms": quant_ms,
         "gemm_int8_tops": 2 * macs / (gemm_ms / 1e3) / 1e12,
+        "wo_gemm_ms": wo_ms,
+        "wo_gemm_int8_tops": 2 * n * DIM * DIM / (wo_ms / 1e3) / 1e12,
     }
-    for w in (wq, wk, wv):
+    for w in (wq, wk, wv, wo):
         w.close()
     ctx.close()
     return {"decode_xb_32k": decode, "prefill_xb_4k": prefill}
@@ -462,7 +513,7 @@ def main() -> int:
                     help="only the 4096-row prefill (a short program for counter passes); "
                          "prints its own JSON line, not the headline one")
     ap.add_argument("--xb-only", action="store_true",
-                    help="only the attention block from xb (Q/K/V projections + attention); "
+                    help="only the attention block from xb (Q/K/V projections, attention, Wo + residual); "
                          "prints its own JSON line, not the headline one")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB: a plain "

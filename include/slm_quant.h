@@ -53,6 +53,16 @@ int slm_quantize_q8_0_dev(slm_attn_ctx* ctx, const float* x, int64_t n, void* bl
 int slm_gemm_q4_0_dev(slm_attn_ctx* ctx, const slm_q4_matrix* w, const float* x,
                       int32_t batch, float* out);
 
+/* A projection followed by the residual add: out[b*rows + r] = res[b*rows + r]
+ * + vec_dot(W row r, q8(x row b)), the gemv_q4_0_arena / gemm_q4_0_arena call
+ * and the residual_add JIT kernel after it (graph.rs:157-164): Wo then
+ * x_mid = x + xb2 (transformer.rs:445-446, batched :595-605) and w_down then
+ * x = x_mid + xb (:477-486, batched :640-650).  Bit-identical to the scalar
+ * dot followed by one f32 add.  res may be out itself (in-place x += W.x_in);
+ * otherwise neither res nor out may overlap x, and out must not overlap res. */
+int slm_gemm_q4_0_residual_dev(slm_attn_ctx* ctx, const slm_q4_matrix* w, const float* x,
+                               int32_t batch, const float* res, float* out);
+
 /* The decode attention block of forward_token_with_kv from the attention
  * RMSNorm output (transformer.rs:413-443): q = Wq.xb, k = Wk.xb, v = Wv.xb
  * (xb quantized once), then slm_attn_decode_dev at `pos`.  wq is dim x dim,
@@ -67,6 +77,23 @@ int slm_attn_decode_xb_dev(slm_attn_ctx* ctx, int32_t layer, int32_t pos, const 
 int slm_attn_prefill_xb_dev(slm_attn_ctx* ctx, int32_t layer, int32_t start, int32_t n,
                             const float* xb, const slm_q4_matrix* wq, const slm_q4_matrix* wk,
                             const slm_q4_matrix* wv, float* out);
+
+/* The attention half of the decode block from the attention RMSNorm output
+ * to the residual stream (transformer.rs:413-446): q, k, v from xb, RoPE, KV
+ * append, attention written back into xb (the reference reuses ws.xb for the
+ * attention output, :432-442), then x_mid = x + Wo.xb.  wo is dim x dim.
+ * x_mid may be x itself; xb must not overlap x, x_mid or the KV cache. */
+int slm_attn_decode_wo_dev(slm_attn_ctx* ctx, int32_t layer, int32_t pos, float* xb,
+                           const slm_q4_matrix* wq, const slm_q4_matrix* wk,
+                           const slm_q4_matrix* wv, const slm_q4_matrix* wo, const float* x,
+                           float* x_mid);
+
+/* The same for a prefill batch of n rows at start (transformer.rs:530-605):
+ * xb, x and x_mid are [n][dim]. */
+int slm_attn_prefill_wo_dev(slm_attn_ctx* ctx, int32_t layer, int32_t start, int32_t n,
+                            float* xb, const slm_q4_matrix* wq, const slm_q4_matrix* wk,
+                            const slm_q4_matrix* wv, const slm_q4_matrix* wo, const float* x,
+                            float* x_mid);
 
 #ifdef __cplusplus
 }

@@ -134,6 +134,9 @@ SIGNATURES = {
     "slm_gemm_q4_0_dev": (ctypes.c_int, [_P, _P, _P, _I, _P]),
     "slm_attn_decode_xb_dev": (ctypes.c_int, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "slm_attn_prefill_xb_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "slm_gemm_q4_0_residual_dev": (ctypes.c_int, [_P, _P, _P, _I, _P, _P]),
+    "slm_attn_decode_wo_dev": (ctypes.c_int, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "slm_attn_prefill_wo_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
 }
 
 _lib = None
@@ -293,6 +296,20 @@ class AttentionContext:
                        wv: "Q4Matrix", out) -> None:
         self._check(self.lib.slm_attn_prefill_xb_dev(self._h, layer, start, n, xb, wq.handle,
                                                      wk.handle, wv.handle, out))
+
+    def gemm_q4_0_residual_dev(self, w: "Q4Matrix", x, batch: int, res, out) -> None:
+        self._check(self.lib.slm_gemm_q4_0_residual_dev(self._h, w.handle, x, batch, res, out))
+
+    def decode_wo_dev(self, layer, pos, xb, wq: "Q4Matrix", wk: "Q4Matrix", wv: "Q4Matrix",
+                      wo: "Q4Matrix", x, x_mid) -> None:
+        self._check(self.lib.slm_attn_decode_wo_dev(self._h, layer, pos, xb, wq.handle,
+                                                    wk.handle, wv.handle, wo.handle, x, x_mid))
+
+    def prefill_wo_dev(self, layer, start, n, xb, wq: "Q4Matrix", wk: "Q4Matrix",
+                       wv: "Q4Matrix", wo: "Q4Matrix", x, x_mid) -> None:
+        self._check(self.lib.slm_attn_prefill_wo_dev(self._h, layer, start, n, xb, wq.handle,
+                                                     wk.handle, wv.handle, wo.handle, x,
+                                                     x_mid))
 
     # -- streams, cache access, timing ------------------------------------------
     def set_stream(self, stream: int | None) -> None:

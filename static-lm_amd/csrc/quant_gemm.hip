@@ -135,6 +135,7 @@ struct QMat {
     const uint8_t* qs;   // [rows][nb][16]
     const uint16_t* d;   // [rows][d_stride], d_stride = nb rounded up to 8
     float* out;          // out[tok * out_stride + row]
+    const float* res;    // nullptr, or the residual added to out (same layout)
     int rows;
     int out_stride;
     int d_stride;
@@ -306,7 +307,10 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
                 s = s + v.w;
             }
             for (; b < nb; ++b) s = s + t[b];
-            M.out[(long)tok * M.out_stride + r] = s;
+            const long o = (long)tok * M.out_stride + r;
+            // the residual_add JIT kernel, out[i] = a[i] + b[i] (graph.rs:157-164)
+            if (M.res) s = M.res[o] + s;
+            M.out[o] = s;
         }
     }
 }
@@ -506,7 +510,9 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int r = wr0 + qr + 16 * rs2 + 4 * g + j;
-                if (r < M.rows) M.out[(long)t * M.out_stride + r] = acc[rs2][ts][j];
+                if (r >= M.rows) continue;
+                const long o = (long)t * M.out_stride + r;
+                M.out[o] = M.res ? M.res[o] + acc[rs2][ts][j] : acc[rs2][ts][j];
             }
         }
 }
@@ -575,8 +581,8 @@ hipError_t launch_q4_gemv(const Q4Job* jobs, int njobs, const float* x, int nb, 
     GemvParams p{};
     int grid = 0;
     for (int i = 0; i < njobs; ++i) {
-        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].rows, jobs[i].out_stride,
-                      q4_scale_stride(nb)};
+        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].res, jobs[i].rows,
+                      jobs[i].out_stride, q4_scale_stride(nb)};
         p.tiles[i] = (jobs[i].rows + kGemvRows - 1) / kGemvRows;
         grid += p.tiles[i];
     }
@@ -593,8 +599,8 @@ hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, cons
     GemmParams p{};
     long tiles = 0;
     for (int i = 0; i < njobs; ++i) {
-        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].rows, jobs[i].out_stride,
-                      q4_scale_stride(nb)};
+        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].res, jobs[i].rows,
+                      jobs[i].out_stride, q4_scale_stride(nb)};
         p.tiles[i] = (jobs[i].rows + kGemmTile - 1) / kGemmTile;
         tiles += p.tiles[i];
     }

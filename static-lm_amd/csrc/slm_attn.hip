@@ -368,8 +368,69 @@ int check_matrix(slm_attn_ctx* c, const slm_q4_matrix* m, int rows, int cols, co
     return SLM_OK;
 }
 
-slm::Q4Job q4_job(const slm_q4_matrix* m, float* out) {
-    return slm::Q4Job{m->qs, m->d, out, m->rows, m->rows};
+slm::Q4Job q4_job(const slm_q4_matrix* m, float* out, const float* res = nullptr) {
+    return slm::Q4Job{m->qs, m->d, out, m->rows, m->rows, res};
+}
+
+// One projection of `batch` rows of x [batch][cols]: GEMV (fused
+// quantization) for a few rows, else quantize + MFMA GEMM.  out (+ res).
+int project(slm_attn_ctx* c, const slm_q4_matrix* w, const float* x, int batch, float* out,
+            const float* res) {
+    const slm::Q4Job job = q4_job(w, out, res);
+    const int nb = w->cols / 32;
+    if (slm::q4_gemv_takes(nb, batch)) {
+        Timed t(c, SLM_K_GEMM);
+        hipError_t e = slm::launch_q4_gemv(&job, 1, x, nb, batch, c->stream);
+        t.done();
+        return launch_status(c, e, "q4 gemv kernel launch");
+    }
+    int rc;
+    if ((rc = ensure_q8(c, (size_t)batch, nb))) return rc;
+    {
+        Timed t(c, SLM_K_QUANT);
+        hipError_t e = slm::launch_quantize_q8_soa(x, batch, nb, c->q8_q, c->q8_d, c->stream);
+        t.done();
+        if (e != hipSuccess) return hip_fail(c, e, "q8 quantize kernel launch");
+    }
+    Timed t(c, SLM_K_GEMM);
+    hipError_t e = slm::launch_q4_gemm(&job, 1, c->q8_q, c->q8_d, nb, batch, c->stream);
+    t.done();
+    return launch_status(c, e, "q4 gemm kernel launch");
+}
+
+// Checks of a projection + residual call: x [batch][cols], res and out
+// [batch][rows]; out may be res itself, otherwise disjoint from it.
+int check_residual_args(slm_attn_ctx* c, const slm_q4_matrix* w, const float* x, int batch,
+                        const float* res, float* out) {
+    int rc;
+    if ((rc = check_dev_ptrs(c, {x, res, out}))) return rc;
+    const size_t in_b = (size_t)batch * w->cols * 4, out_b = (size_t)batch * w->rows * 4;
+    if (overlaps(out, out_b, x, in_b) || overlaps(res, out_b, x, in_b))
+        return fail(c, SLM_ERR_ALIAS, "out and res must not overlap x");
+    if (res != out && overlaps(out, out_b, res, out_b))
+        return fail(c, SLM_ERR_ALIAS, "out must be res itself or not overlap it");
+    if (overlaps(out, out_b, c->kv, c->kv_floats * 4))
+        return fail(c, SLM_ERR_ALIAS, "out must not overlap the KV cache");
+    return SLM_OK;
+}
+
+// Attention rows written into xb, then x_mid = x + Wo.xb: the shared tail of
+// the *_wo entry points.  xb [n][dim] holds the attention output on return.
+int check_wo_args(slm_attn_ctx* c, int n, float* xb, const slm_q4_matrix* wo, const float* x,
+                  float* x_mid) {
+    const slm::Shape& s = c->shape;
+    int rc;
+    if ((rc = check_matrix(c, wo, s.dim, s.dim, "wo")) ||
+        (rc = check_dev_ptrs(c, {xb, x, x_mid})))
+        return rc;
+    const size_t b = (size_t)n * s.dim * 4;
+    if (overlaps(xb, b, x, b) || overlaps(xb, b, x_mid, b))
+        return fail(c, SLM_ERR_ALIAS, "xb must not overlap x or x_mid");
+    if (x_mid != x && overlaps(x_mid, b, x, b))
+        return fail(c, SLM_ERR_ALIAS, "x_mid must be x itself or not overlap it");
+    if (overlaps(x_mid, b, c->kv, c->kv_floats * 4) || overlaps(xb, b, c->kv, c->kv_floats * 4))
+        return fail(c, SLM_ERR_ALIAS, "xb and x_mid must not overlap the KV cache");
+    return SLM_OK;
 }
 
 // q | k | v of n rows from xb [n][dim]: GEMV (fused quantization) for a few
@@ -869,25 +930,18 @@ int slm_gemm_q4_0_dev(slm_attn_ctx* c, const slm_q4_matrix* w, const float* x, i
     if ((rc = check_dev_ptrs(c, {x, out}))) return rc;
     if (overlaps(out, (size_t)batch * w->rows * 4, x, (size_t)batch * w->cols * 4))
         return fail(c, SLM_ERR_ALIAS, "out must not overlap x");
-    const slm::Q4Job job = q4_job(w, out);
-    const int nb = w->cols / 32;
-    if (slm::q4_gemv_takes(nb, batch)) {
-        Timed t(c, SLM_K_GEMM);
-        hipError_t e = slm::launch_q4_gemv(&job, 1, x, nb, batch, c->stream);
-        t.done();
-        return launch_status(c, e, "q4 gemv kernel launch");
-    }
-    if ((rc = ensure_q8(c, (size_t)batch, nb))) return rc;
-    {
-        Timed t(c, SLM_K_QUANT);
-        hipError_t e = slm::launch_quantize_q8_soa(x, batch, nb, c->q8_q, c->q8_d, c->stream);
-        t.done();
-        if (e != hipSuccess) return hip_fail(c, e, "q8 quantize kernel launch");
-    }
-    Timed t(c, SLM_K_GEMM);
-    hipError_t e = slm::launch_q4_gemm(&job, 1, c->q8_q, c->q8_d, nb, batch, c->stream);
-    t.done();
-    return launch_status(c, e, "q4 gemm kernel launch");
+    return project(c, w, x, batch, out, nullptr);
+}
+
+int slm_gemm_q4_0_residual_dev(slm_attn_ctx* c, const slm_q4_matrix* w, const float* x,
+                               int32_t batch, const float* res, float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_matrix(c, w, -1, w ? w->cols : 0, "w"))) return rc;
+    if (batch < 0) return fail(c, SLM_ERR_SHAPE, "batch must not be negative");
+    if (batch == 0) return SLM_OK;
+    if ((rc = check_residual_args(c, w, x, batch, res, out))) return rc;
+    return project(c, w, x, batch, out, res);
 }
 
 int slm_attn_decode_xb_dev(slm_attn_ctx* c, int32_t layer, int32_t pos, const float* xb,
@@ -924,6 +978,38 @@ int slm_attn_prefill_xb_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32
         return fail(c, SLM_ERR_ALIAS, "out must not overlap the context's buffers");
     if ((rc = do_append(c, layer, start, n, k, v))) return rc;
     return do_attend(c, layer, start, n, q, out, true);
+}
+
+int slm_attn_decode_wo_dev(slm_attn_ctx* c, int32_t layer, int32_t pos, float* xb,
+                           const slm_q4_matrix* wq, const slm_q4_matrix* wk,
+                           const slm_q4_matrix* wv, const slm_q4_matrix* wo, const float* x,
+                           float* x_mid) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_pos(c, pos)) ||
+        (rc = check_wo_args(c, 1, xb, wo, x, x_mid)))
+        return rc;
+    float *q, *k, *v;
+    if ((rc = project_qkv(c, 1, xb, wq, wk, wv, &q, &k, &v))) return rc;
+    // stream order: the projections read xb before the attention writes it
+    if ((rc = do_decode(c, layer, pos, q, k, v, xb, true))) return rc;
+    return project(c, wo, xb, 1, x_mid, x);
+}
+
+int slm_attn_prefill_wo_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t n,
+                            float* xb, const slm_q4_matrix* wq, const slm_q4_matrix* wk,
+                            const slm_q4_matrix* wv, const slm_q4_matrix* wo, const float* x,
+                            float* x_mid) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_batch(c, start, n)) ||
+        (rc = check_wo_args(c, n, xb, wo, x, x_mid)))
+        return rc;
+    float *q, *k, *v;
+    if ((rc = project_qkv(c, n, xb, wq, wk, wv, &q, &k, &v))) return rc;
+    if ((rc = do_append(c, layer, start, n, k, v))) return rc;
+    if ((rc = do_attend(c, layer, start, n, q, xb, true))) return rc;
+    return project(c, wo, xb, n, x_mid, x);
 }
 
 }  // extern "C"

@@ -76,13 +76,16 @@ hipError_t launch_prefill_mfma(const Shape& s, const PrefillArgs& a,
 
 // Q4_0 x Q8_0 projections (quant_gemm.hip).  A job is one weight matrix:
 // nibbles [rows][nb][16], f16 scales [rows][q4_scale_stride(nb)],
-// out[tok * out_stride + row].
+// out[tok * out_stride + row].  With res, out = res + product, res laid out
+// like out (res may be out itself: each element is read, then written, by
+// one thread).
 struct Q4Job {
     const uint8_t* qs;
     const uint16_t* d;
     float* out;
     int rows;
     int out_stride;
+    const float* res;
 };
 int q4_max_cols();
 // scale row length: nb rounded up to 8 (the GEMM reads 8 scales per load)

@@ -176,3 +176,119 @@ def test_xb_prefill_gemv_and_gemm_paths_agree():
         ctx.sync()
         assert_bitwise(ctx.kv_read(0, 0, 0, 9), ctx.kv_read(1, 0, 0, 9), "K rows")
         assert_bitwise(ctx.kv_read(0, 1, 0, 9), ctx.kv_read(1, 1, 0, 9), "V rows")
+
+
+RESIDUAL_CASES = [
+    # rows, cols, batch: Wo (dim x dim) and w_down (dim x hidden_dim) shapes
+    (256, 256, 1),        # C1 Wo, GEMV
+    (576, 1536, 1),       # SmolLM2-135M w_down, GEMV
+    (4096, 4096, 1),      # Llama-3-8B Wo, GEMV
+    (4096, 14336, 1),     # Llama-3-8B w_down: nb 448, the longest GEMV row in use
+    (576, 576, 4),        # GEMV batch 4
+    (288, 768, 7),        # MFMA GEMM, ragged row and token tiles
+    (4096, 14336, 65),    # MFMA GEMM, two token tiles
+]
+
+
+@pytest.mark.parametrize("rows,cols,batch", RESIDUAL_CASES)
+@pytest.mark.parametrize("in_place", [False, True])
+def test_projection_plus_residual_bit_exact(ctx, rows, cols, batch, in_place):
+    log(f"residual rows {rows} cols {cols} batch {batch} in_place {in_place}")
+    w = weights([71, rows, cols], rows, cols)
+    x = gen([72, cols, batch], (batch, cols))
+    res = gen([73, rows, batch], (batch, rows)) * np.float32(4.0)
+    want = res + orc.gemm_q4_0_f32(w, x, batch, rows, cols)  # one f32 add per element
+    with P.Q4Matrix(w, rows, cols) as W:
+        xd, rd = dev(x), dev(res)
+        out = rd if in_place else torch.full((batch, rows), float("nan"), device="cuda")
+        ctx.gemm_q4_0_residual_dev(W, xd.data_ptr(), batch, rd.data_ptr(), out.data_ptr())
+        ctx.sync()
+        got = out.cpu().numpy()
+    assert_bitwise(got, want, f"residual {rows}x{cols} batch {batch}")
+
+
+def test_residual_alias_rules(ctx):
+    w = weights(81, 256, 256)
+    with P.Q4Matrix(w, 256, 256) as W:
+        buf = torch.zeros(3 * 256, device="cuda")
+        x, res, out = (buf[i * 256:(i + 1) * 256] for i in range(3))
+        with pytest.raises(P.SlmAttnError) as ei:   # out overlapping x
+            ctx.gemm_q4_0_residual_dev(W, x.data_ptr(), 1, res.data_ptr(), x.data_ptr())
+        assert ei.value.code == P.ERR_ALIAS
+        with pytest.raises(P.SlmAttnError) as ei:   # out partly overlapping res
+            ctx.gemm_q4_0_residual_dev(W, x.data_ptr(), 1, res.data_ptr(),
+                                       buf[300:556].data_ptr())
+        assert ei.value.code == P.ERR_ALIAS
+        ctx.gemm_q4_0_residual_dev(W, x.data_ptr(), 0, 0, 0)  # batch 0: nothing read
+        ctx.sync()
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads,msl,theta", XB_SHAPES)
+def test_attention_block_through_wo(dim, heads, kv_heads, msl, theta):
+    """xb -> q/k/v -> attention (into xb) -> x_mid = x + Wo.xb.
+
+    The attention rows are checked within the attention tolerance against the
+    oracle, the cache rows and x_mid bit for bit (x_mid against the scalar
+    dot of Wo with the attention rows the device produced)."""
+    cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, theta)
+    kvd = cfg.kv_dim
+    log(f"wo block dim {dim} heads {heads}/{kv_heads}")
+    wq = weights([91, dim], dim, dim)
+    wk = weights([92, dim], kvd, dim)
+    wv = weights([93, dim], kvd, dim)
+    wo = weights([94, dim], dim, dim)
+    n_pre, n_dec = 21, 3
+    n = n_pre + n_dec
+    xb = gen([95, dim], (n, dim))
+    x = gen([96, dim], (n, dim)) * np.float32(3.0)
+    om = orc.OracleModel(cfg)
+    q_all = orc.gemm_q4_0_f32(wq, xb, n, dim, dim)
+    k_all = orc.gemm_q4_0_f32(wk, xb, n, kvd, dim)
+    v_all = orc.gemm_q4_0_f32(wv, xb, n, kvd, dim)
+    ref_pre = om.prefill(0, 0, q_all[:n_pre], k_all[:n_pre], v_all[:n_pre])
+    ref_dec = np.stack([om.decode(0, n_pre + s, q_all[n_pre + s], k_all[n_pre + s],
+                                  v_all[n_pre + s]) for s in range(n_dec)])
+    with P.AttentionContext(dim, heads, kv_heads, msl, 1, theta) as ctx, \
+            P.Q4Matrix(wq, dim, dim) as Wq, P.Q4Matrix(wk, kvd, dim) as Wk, \
+            P.Q4Matrix(wv, kvd, dim) as Wv, P.Q4Matrix(wo, dim, dim) as Wo:
+        xbd, xd = dev(xb), dev(x)
+        x_mid = torch.full((n, dim), float("nan"), device="cuda")
+        ctx.prefill_wo_dev(0, 0, n_pre, xbd.data_ptr(), Wq, Wk, Wv, Wo, xd.data_ptr(),
+                           x_mid.data_ptr())
+        for s in range(n_dec):
+            p = n_pre + s
+            if s == n_dec - 1:   # in place: x_mid is x itself
+                x_mid[p].copy_(xd[p])
+                ctx.decode_wo_dev(0, p, xbd[p].data_ptr(), Wq, Wk, Wv, Wo,
+                                  x_mid[p].data_ptr(), x_mid[p].data_ptr())
+            else:
+                ctx.decode_wo_dev(0, p, xbd[p].data_ptr(), Wq, Wk, Wv, Wo, xd[p].data_ptr(),
+                                  x_mid[p].data_ptr())
+        ctx.sync()
+        att = xbd.cpu().numpy()
+        got = x_mid.cpu().numpy()
+        assert_bitwise(ctx.kv_read(0, 0, 0, n), om.k_cache(0)[:n], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, n), om.v_cache(0)[:n], "V rows")
+    assert_close(att[:n_pre], ref_pre, what="prefill attention rows")
+    assert_close(att[n_pre:], ref_dec, what="decode attention rows")
+    want = x + orc.gemm_q4_0_f32(wo, att, n, dim, dim)
+    assert_bitwise(got, want, "x_mid = x + Wo.att")
+
+
+def test_wo_block_argument_checks():
+    dim, heads, kvh = 256, 4, 4
+    w = weights(97, dim, dim)
+    with P.AttentionContext(dim, heads, kvh, 16, 1) as ctx, P.Q4Matrix(w, dim, dim) as W, \
+            P.Q4Matrix(weights(98, 128, dim), 128, dim) as Wbad:
+        buf = torch.zeros(3 * dim, device="cuda")
+        xb, x, xm = (buf[i * dim:(i + 1) * dim] for i in range(3))
+        with pytest.raises(P.SlmAttnError) as ei:
+            ctx.decode_wo_dev(0, 0, xb.data_ptr(), W, W, W, Wbad, x.data_ptr(), xm.data_ptr())
+        assert ei.value.code == P.ERR_SHAPE
+        with pytest.raises(P.SlmAttnError) as ei:   # x_mid on top of xb
+            ctx.decode_wo_dev(0, 0, xb.data_ptr(), W, W, W, W, x.data_ptr(), xb.data_ptr())
+        assert ei.value.code == P.ERR_ALIAS
+        with pytest.raises(P.SlmAttnError) as ei:
+            ctx.prefill_wo_dev(0, 10, 7, xb.data_ptr(), W, W, W, W, x.data_ptr(),
+                               xm.data_ptr())
+        assert ei.value.code == P.ERR_BATCH
