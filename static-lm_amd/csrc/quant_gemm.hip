@@ -104,9 +104,11 @@ __global__ __launch_bounds__(256) void quantize_q8_aos_kernel(const float* x, lo
 // d rows are padded to d_stride (nb rounded up to 8) so the GEMM reads eight
 // blocks' scales with two 128-bit loads.
 
+// With s, the block sums of the quantized values go to s (laid out like d):
+// the GEMV's input, whose nibble dot needs them for the -8 offset.
 __global__ __launch_bounds__(256) void quantize_q8_soa_kernel(const float* x, long nblk, int nb,
                                                               int d_stride, uint32_t* q,
-                                                              float* d) {
+                                                              float* d, int* s) {
     const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 2;
     const int part = threadIdx.x & 3;
     if (i >= nblk) return;  // uniform over the quad
@@ -118,7 +120,9 @@ __global__ __launch_bounds__(256) void quantize_q8_soa_kernel(const float* x, lo
     *reinterpret_cast<uint2*>(q + i * 8 + 2 * part) = qv;
     if (part == 0) {
         const long tok = i / nb;
-        d[tok * d_stride + (i - tok * nb)] = h2f(dbits);
+        const long o = tok * d_stride + (i - tok * nb);
+        d[o] = h2f(dbits);
+        if (s) s[o] = sum;
     }
 }
 
@@ -126,10 +130,13 @@ __global__ __launch_bounds__(256) void quantize_q8_soa_kernel(const float* x, lo
 //
 // Phase 1 quantizes the activation blocks into LDS (four lanes per block;
 // max and integer sums are exact, so any reduction order gives the
-// reference's values).  Phase 2: each wave owns 4 rows, lane l blocks l,
-// l+64, ...; it forms every block term (isum as f32) * (d_w * d_a) and stores
-// it to LDS as [token][row][block].  Phase 3: one lane per (token, row) sums
-// its row's terms in block order, the reference's single f32 accumulator.
+// reference's values).  Then each wave, owning 4 rows, walks the blocks in
+// chunks of 64 (lane l: block 64j + l) in the order the chunks' weight loads
+// were issued: it forms the chunk's block terms (isum as f32) * (d_w * d_a),
+// passes them through its own LDS rows, and lanes 0..4*NT-1 (one per token
+// and row) add them, in block order, to the running sum: the reference's
+// single f32 accumulator.  The ordered sum (nb dependent adds per row)
+// advances while later chunks are still arriving from HBM.
 
 struct QMat {
     const uint8_t* qs;   // [rows][nb][16]
@@ -143,6 +150,9 @@ struct QMat {
 
 constexpr int kGemvRowsPerWave = 4;
 constexpr int kGemvRows = 4 * kGemvRowsPerWave;  // rows per workgroup (256 threads)
+constexpr int kChunk = 64;                       // blocks per chunk, one per lane
+constexpr int kTermStride = kChunk + 4;          // floats per term row in LDS
+constexpr int kPrefetch = 2;                     // chunks in flight ahead of the sums
 
 struct GemvParams {
     QMat m[3];
@@ -153,8 +163,8 @@ struct GemvParams {
     int batch;
 };
 
-__device__ __forceinline__ QMat pick(const GemvParams& p, int m) {
-    return m == 0 ? p.m[0] : (m == 1 ? p.m[1] : p.m[2]);
+__device__ __forceinline__ QMat pick(const QMat (&mm)[3], int m) {
+    return m == 0 ? mm[0] : (m == 1 ? mm[1] : mm[2]);
 }
 
 // Block b's integer dot with unsigned nibbles: sum(nib_i * a_i) - 8 * sum(a).
@@ -171,14 +181,30 @@ __device__ __forceinline__ int block_dot(const uint4 w, const uint32_t (&a)[8], 
     return s - 8 * asum;
 }
 
-
-// Row stride of the block terms in LDS: whole float4s plus 16 bytes, so rows
-// of consecutive lanes start on different banks.
-__host__ __device__ constexpr int gemv_term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
-// Offset (dwords) of the block terms: after q [NT][nb][8], d and sum [NT][nb],
-// rounded up to 16 bytes.
+// Offset (dwords) of the per-wave term rows: after q [NT][nb][8], d and sum
+// [NT][nb], rounded up to 16 bytes.
 __host__ __device__ constexpr int gemv_terms_offset(int nt, int nb) {
     return (nt * nb * 10 + 3) & ~3;
+}
+
+// Adds t[0..cnt) to s in order; a whole chunk reads its 64 terms at once.
+__device__ __forceinline__ float ordered_add(float s, const float* t, int cnt) {
+#pragma clang fp contract(off)
+    if (cnt == kChunk) {
+        float4 v[kChunk / 4];
+#pragma unroll
+        for (int i = 0; i < kChunk / 4; ++i) v[i] = *reinterpret_cast<const float4*>(t + 4 * i);
+#pragma unroll
+        for (int i = 0; i < kChunk / 4; ++i) {
+            s = s + v[i].x;
+            s = s + v[i].y;
+            s = s + v[i].z;
+            s = s + v[i].w;
+        }
+        return s;
+    }
+    for (int i = 0; i < cnt; ++i) s = s + t[i];
+    return s;
 }
 
 template <int NT, int NBL>
@@ -186,14 +212,13 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
 #pragma clang fp contract(off)
     extern __shared__ __align__(16) uint32_t smem[];
     const int nb = p.nb;
-    const int tstride = gemv_term_stride(nb);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     uint32_t* s_q = smem;                                       // [NT][nb][8]
     float* s_d = reinterpret_cast<float*>(smem + NT * nb * 8);  // [NT][nb]
     int* s_sum = reinterpret_cast<int*>(s_d + NT * nb);          // [NT][nb]
-    float* s_t = reinterpret_cast<float*>(smem + gemv_terms_offset(NT, nb));  // [NT][16][tstride]
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    float* s_t = reinterpret_cast<float*>(smem + gemv_terms_offset(NT, nb)) +
+                 wave * (NT * kGemvRowsPerWave * kTermStride);   // this wave's [NT*4][kTermStride]
 
     // workgroup -> (matrix, 16-row tile), uniform
     int tile = blockIdx.x, m = 0;
@@ -201,56 +226,26 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
         tile -= p.tiles[m];
         ++m;
     }
-    const QMat M = pick(p, m);
+    const QMat M = pick(p.m, m);
     const int rw = tile * kGemvRows + wave * kGemvRowsPerWave;  // this wave's first row
 
-    // Activation loads of the first kPrePasses quantization passes go out
-    // before the weight loads, so waiting for them does not wait for the
-    // weights (loads complete in issue order) and the quantization overlaps
-    // the weights' trip from HBM.  Quad q of the workgroup takes blocks q,
-    // q+64, ...; addresses are clamped, results past the end are not stored.
-    constexpr int kPrePasses = 2;
+    // Phase 1 quantizes the activation blocks of every token into LDS (pass
+    // k: blocks 64k + quad).  The activation loads of the first kPre passes
+    // (all of them for one token) go out first, then the weight loads of the
+    // first kPrefetch chunks, so the two trips overlap and the wait for the
+    // activations (loads complete in issue order) does not include the
+    // weights.  Later chunks are loaded kPrefetch chunks ahead of the one
+    // being summed: with every chunk in flight at once the memory system
+    // returns them in no particular order and the first chunk (which the
+    // ordered sums need first) arrives with the last.  Weight addresses are
+    // clamped into the matrix instead of guarded (a guarded load with a zero
+    // fallback makes the compiler wait for each load before the next); terms
+    // of rows or blocks past the end are never used.
+    constexpr int kPre = NT * NBL < 8 ? NT * NBL : 8;
     const int nblk = p.batch * nb;
     const int quad = threadIdx.x >> 2;
     const int part = threadIdx.x & 3;
-    float4 xa[kPrePasses][2];
-#pragma unroll
-    for (int k = 0; k < kPrePasses; ++k) {
-        const float* blk = p.x + (long)min(quad + 64 * k, nblk - 1) * 32 + 8 * part;
-        xa[k][0] = ld4(blk);
-        xa[k][1] = ld4(blk + 4);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
-
-    // Weight loads go out first, all of them before any wait: addresses are
-    // clamped into the matrix instead of guarded (a guarded load with a zero
-    // fallback makes the compiler wait for each load before the next), and
-    // terms of rows or blocks past the end are never read back.
-    uint4 wq[kGemvRowsPerWave][NBL];
-    uint16_t wd[kGemvRowsPerWave][NBL];
-#pragma unroll
-    for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
-        const int r = min(rw + rr, M.rows - 1);
-#pragma unroll
-        for (int j = 0; j < NBL; ++j) {
-            const int b = min(lane + 64 * j, nb - 1);
-            wq[rr][j] = *reinterpret_cast<const uint4*>(M.qs + ((long)r * nb + b) * 16);
-            wd[rr][j] = M.d[(long)r * M.d_stride + b];
-        }
-    }
-
-    // phase 1: activation blocks of every token
-    for (int k = 0; 64 * k < nblk; ++k) {
-        const int idx = quad + 64 * k;
-        float4 f0, f1;
-        if (k < kPrePasses) {
-            f0 = xa[k < kPrePasses ? k : 0][0];
-            f1 = xa[k < kPrePasses ? k : 0][1];
-        } else {
-            const float* blk = p.x + (long)min(idx, nblk - 1) * 32 + 8 * part;
-            f0 = ld4(blk);
-            f1 = ld4(blk + 4);
-        }
+    auto quantize_pass = [&](int idx, float4 f0, float4 f1) {
         uint2 q;
         uint16_t dbits;
         int sum;
@@ -262,55 +257,181 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
                 s_sum[idx] = sum;
             }
         }
+    };
+    float4 xa[kPre][2];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {  // addresses clamped; results past the end not stored
+        const float* blk = p.x + (long)min(quad + 64 * k, nblk - 1) * 32 + 8 * part;
+        xa[k][0] = ld4(blk);
+        xa[k][1] = ld4(blk + 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    uint4 wq[NBL][kGemvRowsPerWave];
+    uint16_t wd[NBL][kGemvRowsPerWave];
+#define SLM_GEMV_ISSUE(j)                                                                    \
+    do {                                                                                     \
+        const int b_ = min(kChunk * (j) + lane, nb - 1);                                     \
+        _Pragma("unroll") for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {                    \
+            const int r_ = min(rw + rr, M.rows - 1);                                         \
+            wq[j][rr] = *reinterpret_cast<const uint4*>(M.qs + ((long)r_ * nb + b_) * 16);   \
+            wd[j][rr] = M.d[(long)r_ * M.d_stride + b_];                                     \
+        }                                                                                    \
+    } while (0)
+#pragma unroll
+    for (int j = 0; j < (kPrefetch < NBL ? kPrefetch : NBL); ++j) SLM_GEMV_ISSUE(j);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+        if (64 * k >= nblk) break;  // uniform
+        quantize_pass(quad + 64 * k, xa[k][0], xa[k][1]);
+    }
+    for (int k = kPre; 64 * k < nblk; ++k) {
+        const int idx = quad + 64 * k;
+        const float* blk = p.x + (long)min(idx, nblk - 1) * 32 + 8 * part;
+        quantize_pass(idx, ld4(blk), ld4(blk + 4));
     }
     __syncthreads();
 
-    // phase 2: block terms
+    // Chunk j: issue chunk j + kPrefetch, then the block terms of chunk j
+    // into this wave's LDS rows, then the ordered sums advance over them.
+    // The term rows are the wave's own and a wave's LDS accesses complete in
+    // program order, so no workgroup barrier is needed between writing and
+    // reading them, nor before the next chunk overwrites them.
+    const bool summer = lane < NT * kGemvRowsPerWave && (lane >> 2) < p.batch;
+    float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NBL; ++j) {
-        const int b = lane + 64 * j;
-        if (b >= nb) break;
+    for (int j = 0; j < NBL; ++j) {  // NBL = ceil(nb / kChunk)
+        if (j + kPrefetch < NBL) SLM_GEMV_ISSUE(j + kPrefetch);
+        __builtin_amdgcn_sched_barrier(0);
+        const int b0 = kChunk * j;
+        const int b = b0 + lane;
+        if (b < nb) {
 #pragma unroll
-        for (int tok = 0; tok < NT; ++tok) {
-            if (tok >= p.batch) break;
-            const int ai = tok * nb + b;
-            const uint4 a0 = *reinterpret_cast<const uint4*>(s_q + ai * 8);
-            const uint4 a1 = *reinterpret_cast<const uint4*>(s_q + ai * 8 + 4);
-            const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            const float da = s_d[ai];
-            const int asum = s_sum[ai];
+            for (int tok = 0; tok < NT; ++tok) {
+                if (tok >= p.batch) break;
+                const int ai = tok * nb + b;
+                const uint4 a0 = *reinterpret_cast<const uint4*>(s_q + ai * 8);
+                const uint4 a1 = *reinterpret_cast<const uint4*>(s_q + ai * 8 + 4);
+                const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                const float da = s_d[ai];
+                const int asum = s_sum[ai];
 #pragma unroll
-            for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
-                const int isum = block_dot(wq[rr][j], a, asum);
-                const float sc = h2f(wd[rr][j]) * da;
-                s_t[(tok * kGemvRows + wave * kGemvRowsPerWave + rr) * tstride + b] =
-                    (float)isum * sc;
+                for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
+                    const int isum = block_dot(wq[j][rr], a, asum);
+                    const float sc = h2f(wd[j][rr]) * da;
+                    s_t[(tok * kGemvRowsPerWave + rr) * kTermStride + lane] = (float)isum * sc;
+                }
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (summer) acc = ordered_add(acc, s_t + lane * kTermStride, min(kChunk, nb - b0));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __syncthreads();
+#undef SLM_GEMV_ISSUE
 
-    // phase 3: one lane per (token, row), blocks in order
-    if (threadIdx.x < NT * kGemvRows) {
-        const int tok = threadIdx.x / kGemvRows;
-        const int row = threadIdx.x - tok * kGemvRows;
-        const int r = tile * kGemvRows + row;
-        if (tok < p.batch && r < M.rows) {
-            const float* t = s_t + (tok * kGemvRows + row) * tstride;
-            float s = 0.0f;
-            int b = 0;
-            for (; b + 4 <= nb; b += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(t + b);
-                s = s + v.x;
-                s = s + v.y;
-                s = s + v.z;
-                s = s + v.w;
-            }
-            for (; b < nb; ++b) s = s + t[b];
-            const long o = (long)tok * M.out_stride + r;
+    if (summer) {
+        const int r = rw + (lane & 3);
+        if (r < M.rows) {
+            const long o = (long)(lane >> 2) * M.out_stride + r;
             // the residual_add JIT kernel, out[i] = a[i] + b[i] (graph.rs:157-164)
-            if (M.res) s = M.res[o] + s;
-            M.out[o] = s;
+            if (M.res) acc = M.res[o] + acc;
+            M.out[o] = acc;
+        }
+    }
+}
+
+// ---- GEMV from pre-quantized activations (one token) ----
+//
+// The activation blocks come quantized (q [nb][32] i8, d and block sums
+// [nb]) from the producing kernel, so a workgroup has no quantization phase
+// and no barrier: each wave streams its 4 rows chunk by chunk (lane l: block
+// 64j + l), loading the weight blocks together with the matching activation
+// blocks kPrefetch chunks ahead, and advances the ordered sums chunk by chunk
+// as in gemv_q4_kernel.
+
+struct GemvQ8Params {
+    QMat m[3];
+    int nmat;
+    int tiles[3];        // kGemvRows-row tiles per matrix
+    const uint32_t* aq;  // [nb][8]
+    const float* ad;     // [nb]
+    const int* as;       // [nb]
+    int nb;
+};
+
+template <int NBL>
+__global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
+#pragma clang fp contract(off)
+    __shared__ __align__(16) float s_t[4][kGemvRowsPerWave][kTermStride];
+    const int nb = p.nb;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int tile = blockIdx.x, m = 0;
+    while (m < p.nmat - 1 && tile >= p.tiles[m]) {
+        tile -= p.tiles[m];
+        ++m;
+    }
+    const QMat M = pick(p.m, m);
+    const int rw = tile * kGemvRows + wave * kGemvRowsPerWave;
+
+    uint4 a0[NBL], a1[NBL];
+    float da[NBL];
+    int as[NBL];
+    uint4 wq[NBL][kGemvRowsPerWave];
+    uint16_t wd[NBL][kGemvRowsPerWave];
+#define SLM_GEMV_ISSUE(j)                                                                    \
+    do {                                                                                     \
+        const int b_ = min(kChunk * (j) + lane, nb - 1);                                     \
+        a0[j] = *reinterpret_cast<const uint4*>(p.aq + (long)b_ * 8);                        \
+        a1[j] = *reinterpret_cast<const uint4*>(p.aq + (long)b_ * 8 + 4);                    \
+        da[j] = p.ad[b_];                                                                    \
+        as[j] = p.as[b_];                                                                    \
+        _Pragma("unroll") for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {                    \
+            const int r_ = min(rw + rr, M.rows - 1);                                         \
+            wq[j][rr] = *reinterpret_cast<const uint4*>(M.qs + ((long)r_ * nb + b_) * 16);   \
+            wd[j][rr] = M.d[(long)r_ * M.d_stride + b_];                                     \
+        }                                                                                    \
+    } while (0)
+#pragma unroll
+    for (int j = 0; j < (kPrefetch < NBL ? kPrefetch : NBL); ++j) SLM_GEMV_ISSUE(j);
+
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) {  // NBL = ceil(nb / kChunk)
+        if (j + kPrefetch < NBL) SLM_GEMV_ISSUE(j + kPrefetch);
+        __builtin_amdgcn_sched_barrier(0);
+        const int b0 = kChunk * j;
+        if (b0 + lane < nb) {
+            const uint32_t a[8] = {a0[j].x, a0[j].y, a0[j].z, a0[j].w,
+                                   a1[j].x, a1[j].y, a1[j].z, a1[j].w};
+#pragma unroll
+            for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
+                const int isum = block_dot(wq[j][rr], a, as[j]);
+                s_t[wave][rr][lane] = (float)isum * (h2f(wd[j][rr]) * da[j]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < kGemvRowsPerWave) acc = ordered_add(acc, &s_t[wave][lane][0], min(kChunk, nb - b0));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+#undef SLM_GEMV_ISSUE
+
+    if (lane < kGemvRowsPerWave) {
+        const int r = rw + lane;
+        if (r < M.rows) {
+            // the residual_add JIT kernel, out[i] = a[i] + b[i] (graph.rs:157-164)
+            if (M.res) acc = M.res[r] + acc;
+            M.out[r] = acc;
         }
     }
 }
@@ -520,21 +641,25 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
 #undef SLM_GEMM_STORE_STAGE
 
 size_t gemv_lds_bytes(int nt, int nb) {
-    return ((size_t)gemv_terms_offset(nt, nb) + (size_t)nt * kGemvRows * gemv_term_stride(nb)) * 4;
+    return ((size_t)gemv_terms_offset(nt, nb) + (size_t)nt * kGemvRows * kTermStride) * 4;
 }
 
 template <int NT, int NBL>
 hipError_t launch_gemv_t(const GemvParams& p, int grid, hipStream_t st) {
-    const size_t lds = gemv_lds_bytes(NT, p.nb);
-    if (lds > 64 * 1024) {
-        // above the default dynamic-LDS limit (at most 106 KiB of the 160 KiB)
-        const hipError_t e = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(gemv_q4_kernel<NT, NBL>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
+    if constexpr (NT > 1 && NBL > 4) {
+        return hipErrorInvalidValue;  // batches above 1 take rows of at most 256 blocks
+    } else {
+        const size_t lds = gemv_lds_bytes(NT, p.nb);
+        if (lds > 64 * 1024) {
+            // above the default dynamic-LDS limit
+            const hipError_t e = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(gemv_q4_kernel<NT, NBL>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((gemv_q4_kernel<NT, NBL>), dim3(grid), dim3(256), lds, st, p);
+        return hipGetLastError();
     }
-    hipLaunchKernelGGL((gemv_q4_kernel<NT, NBL>), dim3(grid), dim3(256), lds, st, p);
-    return hipGetLastError();
 }
 
 template <int NT>
@@ -543,8 +668,12 @@ hipError_t launch_gemv_nt(const GemvParams& p, int grid, hipStream_t st) {
     switch (nbl) {
         case 1: return launch_gemv_t<NT, 1>(p, grid, st);
         case 2: return launch_gemv_t<NT, 2>(p, grid, st);
-        case 3: case 4: return launch_gemv_t<NT, 4>(p, grid, st);
-        case 5: case 6: case 7: case 8: return launch_gemv_t<NT, 8>(p, grid, st);
+        case 3: return launch_gemv_t<NT, 3>(p, grid, st);
+        case 4: return launch_gemv_t<NT, 4>(p, grid, st);
+        case 5: return launch_gemv_t<NT, 5>(p, grid, st);
+        case 6: return launch_gemv_t<NT, 6>(p, grid, st);
+        case 7: return launch_gemv_t<NT, 7>(p, grid, st);
+        case 8: return launch_gemv_t<NT, 8>(p, grid, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -563,11 +692,11 @@ hipError_t launch_quantize_q8_aos(const float* x, long nblk, uint8_t* out, hipSt
 int q4_scale_stride(int nb) { return (nb + kScaleChunk - 1) / kScaleChunk * kScaleChunk; }
 
 hipError_t launch_quantize_q8_soa(const float* x, long ntok, int nb, uint32_t* q, float* d,
-                                  hipStream_t st) {
+                                  int* sums, hipStream_t st) {
     const long nblk = ntok * nb;
     if (nblk <= 0) return hipSuccess;
     hipLaunchKernelGGL(quantize_q8_soa_kernel, dim3((unsigned)((nblk + 63) / 64)), dim3(256),
-                       0, st, x, nblk, nb, q4_scale_stride(nb), q, d);
+                       0, st, x, nblk, nb, q4_scale_stride(nb), q, d, sums);
     return hipGetLastError();
 }
 
@@ -591,6 +720,33 @@ hipError_t launch_q4_gemv(const Q4Job* jobs, int njobs, const float* x, int nb, 
     p.nb = nb;
     p.batch = batch;
     return batch == 1 ? launch_gemv_nt<1>(p, grid, st) : launch_gemv_nt<4>(p, grid, st);
+}
+
+hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
+                             const int* as, int nb, hipStream_t st) {
+    if (njobs < 1 || njobs > 3 || nb < 1 || nb > 8 * kChunk) return hipErrorInvalidValue;
+    GemvQ8Params p{};
+    int grid = 0;
+    for (int i = 0; i < njobs; ++i) {
+        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].res, jobs[i].rows,
+                      jobs[i].out_stride, q4_scale_stride(nb)};
+        p.tiles[i] = (jobs[i].rows + kGemvRows - 1) / kGemvRows;
+        grid += p.tiles[i];
+    }
+    p.nmat = njobs;
+    p.aq = aq;
+    p.ad = ad;
+    p.as = as;
+    p.nb = nb;
+    switch ((nb + kChunk - 1) / kChunk) {
+#define SLM_GEMV_Q8_CASE(n) \
+    case n: hipLaunchKernelGGL(gemv_q8in_kernel<n>, dim3(grid), dim3(256), 0, st, p); break;
+        SLM_GEMV_Q8_CASE(1) SLM_GEMV_Q8_CASE(2) SLM_GEMV_Q8_CASE(3) SLM_GEMV_Q8_CASE(4)
+        SLM_GEMV_Q8_CASE(5) SLM_GEMV_Q8_CASE(6) SLM_GEMV_Q8_CASE(7) SLM_GEMV_Q8_CASE(8)
+#undef SLM_GEMV_Q8_CASE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,

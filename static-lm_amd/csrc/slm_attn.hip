@@ -388,7 +388,7 @@ int project(slm_attn_ctx* c, const slm_q4_matrix* w, const float* x, int batch, 
     if ((rc = ensure_q8(c, (size_t)batch, nb))) return rc;
     {
         Timed t(c, SLM_K_QUANT);
-        hipError_t e = slm::launch_quantize_q8_soa(x, batch, nb, c->q8_q, c->q8_d, c->stream);
+        hipError_t e = slm::launch_quantize_q8_soa(x, batch, nb, c->q8_q, c->q8_d, nullptr, c->stream);
         t.done();
         if (e != hipSuccess) return hip_fail(c, e, "q8 quantize kernel launch");
     }
@@ -462,7 +462,7 @@ int project_qkv(slm_attn_ctx* c, int n, const float* xb, const slm_q4_matrix* wq
     if ((rc = ensure_q8(c, (size_t)n, nb))) return rc;
     {
         Timed t(c, SLM_K_QUANT);
-        hipError_t e = slm::launch_quantize_q8_soa(xb, n, nb, c->q8_q, c->q8_d, c->stream);
+        hipError_t e = slm::launch_quantize_q8_soa(xb, n, nb, c->q8_q, c->q8_d, nullptr, c->stream);
         t.done();
         if (e != hipSuccess) return hip_fail(c, e, "q8 quantize kernel launch");
     }

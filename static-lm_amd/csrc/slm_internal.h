@@ -96,12 +96,17 @@ bool q4_gemv_takes(int nb, int batch);
 // quantize_row_q8_0 into 34-byte blocks
 hipError_t launch_quantize_q8_aos(const float* x, long nblk, uint8_t* out, hipStream_t st);
 // quantize_row_q8_0 of ntok rows of nb blocks into q [ntok][nb][32] i8 and
-// d [ntok][q4_scale_stride(nb)] f32 (the GEMM's input)
+// d [ntok][q4_scale_stride(nb)] f32 (the GEMM's input); with sums, also the
+// blocks' sums of quantized values, laid out like d (the GEMV's input)
 hipError_t launch_quantize_q8_soa(const float* x, long ntok, int nb, uint32_t* q, float* d,
-                                  hipStream_t st);
+                                  int* sums, hipStream_t st);
 // a batch q4_gemv_takes(): quantizes x [batch][nb*32] itself
 hipError_t launch_q4_gemv(const Q4Job* jobs, int njobs, const float* x, int nb, int batch,
                           hipStream_t st);
+// one token from pre-quantized activations (q [nb][8] u32, d and block sums
+// [nb]); nb at most 512
+hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
+                             const int* as, int nb, hipStream_t st);
 // any batch, from pre-quantized activations
 hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
                           int nb, int batch, hipStream_t st);
