@@ -20,7 +20,8 @@
  *     reference behaviour.
  *   - A context is not thread-safe (it mirrors `&mut AlignedArena`); separate
  *     contexts are independent.  Each context owns one HIP stream (default
- *     priority) unless slm_attn_set_stream() hands it another.
+ *     priority, blocking: ordered with the legacy default stream) unless
+ *     slm_attn_set_stream() hands it another.
  *   - Host-pointer entry points are synchronous and borrow their buffers for
  *     the call only.  *_dev entry points take device pointers, are enqueued on
  *     the context stream and return without waiting.
@@ -183,7 +184,9 @@ enum {
     SLM_K_ROPE = 4,    /* standalone rope */
     SLM_K_QUANT = 5,   /* Q8_0 activation quantization (slm_quant.h) */
     SLM_K_GEMM = 6,    /* Q4_0 x Q8_0 GEMV / GEMM (slm_quant.h) */
-    SLM_K_COUNT = 7
+    SLM_K_NORM = 7,    /* RMSNorm / L2 norm (slm_layer.h) */
+    SLM_K_ELEM = 8,    /* SwiGLU, residual add, embedding rows, argmax (slm_layer.h) */
+    SLM_K_COUNT = 9
 };
 typedef struct slm_kernel_stat {
     int64_t launches;

@@ -59,7 +59,23 @@ _SIGS = {
     "orc_vec_dot_q4_0_q8_0_scalar": (ctypes.c_float, [_U8, _U8, _SZ]),
     "orc_vec_dot_q4_0_q8_0_avx2": (ctypes.c_float, [_U8, _U8, _SZ]),
     "orc_gemm_q4_0": (None, [_U8, _U8, _F, _I, _I, _I, _I]),
+    "orc_jit_rmsnorm_scale": (ctypes.c_float, [_F, _SZ, ctypes.c_float]),
+    "orc_jit_rmsnorm": (None, [_F, _F, _SZ, ctypes.c_float, _F]),
+    "orc_jit_silu": (ctypes.c_float, [ctypes.c_float]),
+    "orc_jit_swiglu": (None, [_F, _F, _SZ, _F]),
+    "orc_jit_residual_add": (None, [_F, _F, _SZ, _F]),
+    "orc_jit_l2_norm": (None, [_F, _SZ, ctypes.c_float, _F]),
+    "orc_scalar_rmsnorm": (None, [_F, _F, _SZ, ctypes.c_float, _F]),
+    "orc_layer_forward_batch": (None, [_C, _I, ctypes.c_float, ctypes.c_void_p, _F, _F, _F,
+                                       _I, _I, _I, _F]),
 }
+
+
+class OrcLayerWeights(ctypes.Structure):
+    _fields_ = [
+        ("rms_att", _F), ("wq", _U8), ("wk", _U8), ("wv", _U8), ("wo", _U8),
+        ("rms_ffn", _F), ("w_gate", _U8), ("w_up", _U8), ("w_down", _U8),
+    ]
 
 _lib = None
 
@@ -241,6 +257,19 @@ class OracleModel:
             kc[p] = apply_rope_cached(k_rows[r], self.cos[p], self.sin[p], self.cfg.head_dim)
             vc[p] = v_rows[r]
 
+    def layer_forward(self, layer: int, start: int, x, w: "LayerWeights", eps: float) -> np.ndarray:
+        """forward_batch_with_kv (transformer.rs:491-651) of x [n][dim] at
+        rows start..start+n-1; n = 1 is forward_token_with_kv.  Returns the
+        new residual stream; the cache rows are written like the reference's."""
+        x = np.array(_f32(x).reshape(-1, self.cfg.dim), copy=True)
+        n = x.shape[0]
+        c = self.cfg.c()
+        cw = w.c()
+        lib().orc_layer_forward_batch(ctypes.byref(c), w.hidden_dim, eps, ctypes.byref(cw),
+                                      _p(self.kv), _p(self.cos), _p(self.sin), layer, start, n,
+                                      _p(x))
+        return x
+
     def rotated_q(self, q_row, pos: int) -> np.ndarray:
         return apply_rope_cached(q_row, self.cos[pos], self.sin[pos], self.cfg.head_dim)
 
@@ -332,3 +361,87 @@ def gemm_q4_0_f32(w: np.ndarray, x, batch: int, rows: int, cols: int,
     """gemm_q4_0_arena (kernels.rs:398-415): quantize x [batch][cols] to Q8_0,
     then gemm_q4_0."""
     return gemm_q4_0(w, quantize_q8_0(x), batch, rows, cols, avx2)
+
+
+# ---- JIT normalisation / activation kernels and the block (layer.c) ----
+
+def jit_rmsnorm(x, w, eps: float) -> np.ndarray:
+    """FuseGraph::rmsnorm (graph.rs:141-156) over each row of x."""
+    x = _f32(x)
+    w = _f32(w)
+    rows = x.reshape(-1, w.size)
+    out = np.empty_like(rows)
+    for r in range(rows.shape[0]):
+        row = np.ascontiguousarray(rows[r])
+        o = np.empty_like(row)
+        lib().orc_jit_rmsnorm(_p(row), _p(w), w.size, eps, _p(o))
+        out[r] = o
+    return out.reshape(x.shape)
+
+
+def jit_rmsnorm_scale(x, eps: float) -> float:
+    x = _f32(x)
+    return float(lib().orc_jit_rmsnorm_scale(_p(x), x.size, eps))
+
+
+def scalar_rmsnorm(x, w, eps: float) -> np.ndarray:
+    """The reference tests' scalar_rmsnorm (transformer.rs:978-985)."""
+    x, w = _f32(x), _f32(w)
+    out = np.empty_like(x)
+    lib().orc_scalar_rmsnorm(_p(x), _p(w), x.size, eps, _p(out))
+    return out
+
+
+def jit_silu(v) -> np.ndarray:
+    v = _f32(v)
+    return np.array([lib().orc_jit_silu(float(t)) for t in v.ravel()], np.float32).reshape(v.shape)
+
+
+def jit_swiglu(gate, up) -> np.ndarray:
+    """FuseGraph::swiglu (graph.rs:131-139)."""
+    gate, up = _f32(gate), _f32(up)
+    out = np.empty_like(gate)
+    lib().orc_jit_swiglu(_p(gate), _p(up), gate.size, _p(out))
+    return out
+
+
+def jit_residual_add(a, b) -> np.ndarray:
+    a, b = _f32(a), _f32(b)
+    out = np.empty_like(a)
+    lib().orc_jit_residual_add(_p(a), _p(b), a.size, _p(out))
+    return out
+
+
+def jit_l2_norm(x, eps: float) -> np.ndarray:
+    """FuseGraph::l2_norm (graph.rs:182-193)."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_jit_l2_norm(_p(x), x.size, eps, _p(out))
+    return out
+
+
+@dataclass
+class LayerWeights:
+    """TransformerWeights (transformer.rs:36-47): f32 norm scales and
+    BlockQ4_0 matrices as uint8 arrays of 18-byte blocks."""
+    rms_att: np.ndarray
+    wq: np.ndarray
+    wk: np.ndarray
+    wv: np.ndarray
+    wo: np.ndarray
+    rms_ffn: np.ndarray
+    w_gate: np.ndarray
+    w_up: np.ndarray
+    w_down: np.ndarray
+    hidden_dim: int
+
+    def c(self) -> OrcLayerWeights:
+        for name in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+            a = getattr(self, name)
+            assert a.dtype == np.uint8 and a.flags.c_contiguous
+        for name in ("rms_att", "rms_ffn"):
+            a = getattr(self, name)
+            assert a.dtype == np.float32 and a.flags.c_contiguous
+        return OrcLayerWeights(_p(self.rms_att), _u8(self.wq), _u8(self.wk), _u8(self.wv),
+                               _u8(self.wo), _p(self.rms_ffn), _u8(self.w_gate),
+                               _u8(self.w_up), _u8(self.w_down))

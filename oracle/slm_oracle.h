@@ -135,6 +135,43 @@ float orc_vec_dot_q4_0_q8_0_avx2(const uint8_t* w, const uint8_t* a, size_t nblo
 void orc_gemm_q4_0(const uint8_t* w, const uint8_t* x_q8, float* out, int batch, int rows,
                    int cols, int avx2);
 
+/* ---- JIT normalisation / activation kernels and the transformer block
+ * (layer.c; graph.rs:130-193 lowered by lower.rs:212-480) ---- */
+/* RMSNorm's scale 1 / sqrt(sum(x^2) * (1/n) + eps), JIT reduction order. */
+float orc_jit_rmsnorm_scale(const float* x, size_t n, float eps);
+/* FuseGraph::rmsnorm: out[i] = (x[i] * rms) * w[i]. */
+void orc_jit_rmsnorm(const float* x, const float* w, size_t n, float eps, float* out);
+/* SiLU lowering: v / (1 + exp(-v)), polynomial exp. */
+float orc_jit_silu(float v);
+/* FuseGraph::swiglu: out[i] = silu(gate[i]) * up[i]. */
+void orc_jit_swiglu(const float* gate, const float* up, size_t n, float* out);
+/* FuseGraph::residual_add: out[i] = a[i] + b[i]. */
+void orc_jit_residual_add(const float* a, const float* b, size_t n, float* out);
+/* FuseGraph::l2_norm: out[i] = x[i] * (1 / sqrt(sum(x^2) + eps)). */
+void orc_jit_l2_norm(const float* x, size_t n, float eps, float* out);
+/* The reference tests' scalar_rmsnorm (transformer.rs:978-985). */
+void orc_scalar_rmsnorm(const float* x, const float* w, size_t n, float eps, float* out);
+
+/* One layer's weights: f32 norm scales and BlockQ4_0 matrices (18-byte
+ * blocks, row-major) as TransformerWeights holds them (transformer.rs:36-47). */
+typedef struct {
+    const float* rms_att;
+    const uint8_t* wq;
+    const uint8_t* wk;
+    const uint8_t* wv;
+    const uint8_t* wo;
+    const float* rms_ffn;
+    const uint8_t* w_gate;
+    const uint8_t* w_up;
+    const uint8_t* w_down;
+} orc_layer_weights;
+
+/* forward_batch_with_kv (transformer.rs:491-651) on x [n][dim] in place;
+ * n = 1 is forward_token_with_kv (391-487).  GEMMs use the scalar dot. */
+void orc_layer_forward_batch(const orc_config* cfg, int hidden_dim, float eps,
+                             const orc_layer_weights* w, float* kv, const float* cos_tab,
+                             const float* sin_tab, int layer, int start, int n, float* x);
+
 #ifdef __cplusplus
 }
 #endif

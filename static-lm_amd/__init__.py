@@ -26,6 +26,7 @@ LIB_PATH = PKG_DIR / "libslm_attn.so"
 HEADER_PATH = PKG_DIR.parent / "include" / "slm_attn.h"
 CALIB_HEADER_PATH = PKG_DIR.parent / "include" / "slm_calib.h"
 QUANT_HEADER_PATH = PKG_DIR.parent / "include" / "slm_quant.h"
+LAYER_HEADER_PATH = PKG_DIR.parent / "include" / "slm_layer.h"
 
 SLM_OK = 0
 ERRORS = {
@@ -43,7 +44,8 @@ ERRORS = {
 (ERR_CONFIG, ERR_POS, ERR_BATCH, ERR_LAYER, ERR_ALIAS, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED,
  ERR_DEVICE, ERR_SHAPE) = (-1, -2, -3, -4, -5, -6, -7, -8, -9, -10)
 
-KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope", "quant", "gemm")
+KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope", "quant", "gemm", "norm",
+                "elem")
 
 
 class SlmAttnError(RuntimeError):
@@ -137,7 +139,18 @@ SIGNATURES = {
     "slm_gemm_q4_0_residual_dev": (ctypes.c_int, [_P, _P, _P, _I, _P, _P]),
     "slm_attn_decode_wo_dev": (ctypes.c_int, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "slm_attn_prefill_wo_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "slm_rmsnorm_dev": (ctypes.c_int, [_P, _P, _P, _I, _I, ctypes.c_float, _P]),
+    "slm_l2_norm_dev": (ctypes.c_int, [_P, _P, _I, _I, ctypes.c_float, _P]),
+    "slm_swiglu_dev": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P]),
+    "slm_residual_add_dev": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P]),
+    "slm_layer_forward_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, ctypes.c_float, _P]),
 }
+
+
+class LayerWeightsC(ctypes.Structure):
+    """slm_layer_weights (include/slm_layer.h)."""
+    _fields_ = [("rms_att", _P), ("wq", _P), ("wk", _P), ("wv", _P), ("wo", _P),
+                ("rms_ffn", _P), ("w_gate", _P), ("w_up", _P), ("w_down", _P)]
 
 _lib = None
 
@@ -311,6 +324,24 @@ class AttentionContext:
                                                      wk.handle, wv.handle, wo.handle, x,
                                                      x_mid))
 
+    def rmsnorm_dev(self, x, w, rows: int, n: int, eps: float, out) -> None:
+        self._check(self.lib.slm_rmsnorm_dev(self._h, x, w, rows, n, eps, out))
+
+    def l2_norm_dev(self, x, rows: int, n: int, eps: float, out) -> None:
+        self._check(self.lib.slm_l2_norm_dev(self._h, x, rows, n, eps, out))
+
+    def swiglu_dev(self, gate, up, n: int, out) -> None:
+        self._check(self.lib.slm_swiglu_dev(self._h, gate, up, n, out))
+
+    def residual_add_dev(self, a, b, n: int, out) -> None:
+        self._check(self.lib.slm_residual_add_dev(self._h, a, b, n, out))
+
+    def layer_forward_dev(self, layer: int, start: int, n: int, weights: "LayerWeights",
+                          rms_eps: float, x) -> None:
+        c = weights.c()
+        self._check(self.lib.slm_layer_forward_dev(self._h, layer, start, n, ctypes.byref(c),
+                                                   rms_eps, x))
+
     # -- streams, cache access, timing ------------------------------------------
     def set_stream(self, stream: int | None) -> None:
         self._check(self.lib.slm_attn_set_stream(self._h, stream or None))
@@ -402,11 +433,30 @@ class Q4Matrix:
             pass
 
 
+class LayerWeights:
+    """slm_layer_weights (include/slm_layer.h): the two RMSNorm scale vectors
+    as device pointers (their memory is the caller's to keep alive) and the
+    seven Q4Matrix projections of one layer."""
+
+    def __init__(self, rms_att: int, wq: Q4Matrix, wk: Q4Matrix, wv: Q4Matrix, wo: Q4Matrix,
+                 rms_ffn: int, w_gate: Q4Matrix, w_up: Q4Matrix, w_down: Q4Matrix):
+        self.rms_att, self.rms_ffn = rms_att, rms_ffn
+        self.mats = (wq, wk, wv, wo, w_gate, w_up, w_down)
+
+    def c(self) -> "LayerWeightsC":
+        wq, wk, wv, wo, w_gate, w_up, w_down = (m.handle for m in self.mats)
+        return LayerWeightsC(self.rms_att, wq, wk, wv, wo, self.rms_ffn, w_gate, w_up, w_down)
+
+    def close(self) -> None:
+        for m in self.mats:
+            m.close()
+
+
 def header_functions(*headers: os.PathLike | str) -> list[str]:
     """Names of the functions the given headers (default: every include/*.h) declare."""
     import re
 
-    paths = headers or (HEADER_PATH, CALIB_HEADER_PATH, QUANT_HEADER_PATH)
+    paths = headers or (HEADER_PATH, CALIB_HEADER_PATH, QUANT_HEADER_PATH, LAYER_HEADER_PATH)
     names = set()
     for h in paths:
         names |= set(re.findall(r"\b(slm_[a-z0-9_]+)\s*\(", Path(h).read_text()))

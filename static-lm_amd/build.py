@@ -21,8 +21,8 @@ LIB = PKG_DIR / "libslm_attn.so"
 HOST_DEMO = PKG_DIR / "slm_host_demo"
 BUILD_DIR = PKG_DIR / "_build"
 
-HIP_SOURCES = ["slm_attn.hip", "rope_append.hip", "attn_decode.hip", "prefill_mfma.hip",
-               "quant_gemm.hip", "calib.hip"]
+HIP_SOURCES = ["slm_attn.hip", "slm_layer.hip", "rope_append.hip", "attn_decode.hip", "prefill_mfma.hip",
+               "quant_gemm.hip", "norm_act.hip", "calib.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [

@@ -1,0 +1,413 @@
+// The JIT kernels around the projections, for gfx950: RMSNorm, L2 norm,
+// SwiGLU and the residual add (FuseGraph, src/jit/graph.rs:130-193), plus
+// the token-embedding row lookup (dequantize_row_q4_0, blocks.rs:85-99) and
+// greedy argmax (sample_argmax, transformer.rs:654-666).
+//
+// Bit-exactness.  lower_fuse_graph (src/jit/lower.rs:212-480) evaluates a
+// reduction as four lane accumulators over i < n & ~3 (lane k takes
+// i = k mod 4, in order), then (l0 + l1) + (l2 + l3), then a scalar tail in
+// order; scalars derived from the reduction are hoisted, and the store pass
+// applies the elementwise ops per element.  Every f32 operation is IEEE with
+// no contraction (Cranelift never fuses), so the kernels keep the same
+// operations in the same order: each of the four lane sums is one dependent
+// chain of n/4 adds run by one lane, and division and square root are the
+// correctly rounded ones.  The normalized rows can be emitted directly as
+// Q8_0 blocks (quantize_row_q8_0's arithmetic) for the projection that reads
+// them, which is what the reference's next call does with them.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "attn_common.h"
+#include "quant_common.h"
+#include "slm_internal.h"
+
+namespace slm {
+namespace {
+
+constexpr int kNormThreads = 256;
+
+// emit_exp_f32x4 (lower.rs:22-65), one lane: clamp to [-87.3, 88.3],
+// n = nearest(x * log2 e) (ties to even), Cody-Waite reduction with the two
+// ln 2 constants, degree-5 Horner polynomial, times 2^n built from the
+// exponent bits.  (fmaxf/fminf return the non-NaN operand where Cranelift's
+// fmax/fmin propagate NaN; the paths here never feed them NaN from finite
+// inputs.)
+__device__ __forceinline__ float jit_exp(float x) {
+#pragma clang fp contract(off)
+    float xc = fmaxf(x, -87.3f);
+    xc = fminf(xc, 88.3f);
+    const float fx = xc * 1.44269504088896340736f;
+    const float n = rintf(fx);
+    const float n_hi = n * 0.69314575f;
+    const float n_lo = n * 1.4286068e-6f;
+    const float r_hi = xc - n_hi;
+    const float r = r_hi - n_lo;
+    float p = r * (1.0f / 120.0f);
+    p = p + (1.0f / 24.0f);
+    p = r * p;
+    p = p + (1.0f / 6.0f);
+    p = r * p;
+    p = p + 0.5f;
+    p = r * p;
+    p = p + 1.0f;
+    p = r * p;
+    const float poly = p + 1.0f;
+    const int ni = (int)n;  // |n| <= 128 after the clamp
+    return poly * __int_as_float((ni + 127) << 23);
+}
+
+// Correctly rounded f32 square root (what Cranelift's `sqrt` is, x86
+// sqrtps).  v_sqrt_f32 is within 1 ulp; the exact residuals x - s'*s of its
+// neighbours s' = s -/+ 1 ulp (one fused multiply-add each, exact) tell
+// whether the rounded root is s or a neighbour.  Tiny inputs are scaled by
+// 2^32 first (root scaled by 2^16) so the residuals stay representable.
+__device__ __forceinline__ float sqrt_rn(float x) {
+    const bool tiny = x < 0x1.0p-96f;
+    const float xs = tiny ? x * 0x1.0p+32f : x;
+    float s = __builtin_amdgcn_sqrtf(xs);
+    const float s_dn = __int_as_float(__float_as_int(s) - 1);
+    const float s_up = __int_as_float(__float_as_int(s) + 1);
+    const float r_dn = __builtin_fmaf(-s_dn, s, xs);
+    const float r_up = __builtin_fmaf(-s_up, s, xs);
+    s = r_dn <= 0.0f ? s_dn : s;
+    s = r_up > 0.0f ? s_up : s;
+    s = tiny ? s * 0x1.0p-16f : s;
+    // zero, infinity and NaN pass through unchanged
+    return (xs == 0.0f || xs == __builtin_inff() || xs != xs) ? __builtin_amdgcn_sqrtf(xs) : s;
+}
+
+// SiLU lowering (lower.rs:85-91): v / (1 + exp(-v)).
+__device__ __forceinline__ float jit_silu(float v) {
+#pragma clang fp contract(off)
+    const float e = jit_exp(-v);
+    const float den = 1.0f + e;
+    return __fdiv_rn(v, den);
+}
+
+// ---- RMSNorm / L2 norm: one workgroup per row ----
+//
+// The squares go to LDS transposed, s_sq[k][i] = x[4i + k]^2, so lane k of
+// wave 0 reads its chain contiguously; lanes 0..3 run the four chains, lane 0
+// combines them and the tail, and computes the scale.  Then every thread
+// writes its share of the output (f32 and/or Q8_0 blocks).
+
+struct NormArgs {
+    const float* x;   // [rows][n], row stride x_stride floats
+    long x_stride;
+    const float* w;   // [n] (RMSNorm) or nullptr (L2 norm)
+    int n;
+    float eps;
+    float* out;       // [rows][n], row stride out_stride, or nullptr
+    long out_stride;
+    Q8Out q8;         // Q8_0 output of each row, or q8.q == nullptr
+};
+
+__host__ __device__ constexpr int norm_sq_stride(int n) { return n / 4 + 4; }
+
+template <bool RMS>
+__global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(NormArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) float s_sq[];  // [4][norm_sq_stride(n)]
+    __shared__ float s_part[4];
+    __shared__ float s_tail[4];
+    __shared__ float s_scale;
+    const int n = a.n;
+    const int vq = n / 4;  // full groups of four
+    const int st = norm_sq_stride(n);
+    const float* x = a.x + (long)blockIdx.x * a.x_stride;
+    const int tid = threadIdx.x;
+
+    // squares (x2 = mul(x, x)), transposed
+    for (int i = tid; i < vq; i += kNormThreads) {
+        const float4 v = ld4(x + 4 * i);
+        s_sq[0 * st + i] = v.x * v.x;
+        s_sq[1 * st + i] = v.y * v.y;
+        s_sq[2 * st + i] = v.z * v.z;
+        s_sq[3 * st + i] = v.w * v.w;
+    }
+    if (tid < n - 4 * vq) {
+        const float v = x[4 * vq + tid];
+        s_tail[tid] = v * v;
+    }
+    __syncthreads();
+
+    if (tid < 4) {  // the four lane accumulators, in order
+        const float* t = s_sq + tid * st;
+        float acc = 0.0f;
+        int i = 0;
+        for (; i + 16 <= vq; i += 16) {
+            float4 c[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c[k] = *reinterpret_cast<const float4*>(t + i + 4 * k);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                acc = acc + c[k].x;
+                acc = acc + c[k].y;
+                acc = acc + c[k].z;
+                acc = acc + c[k].w;
+            }
+        }
+        for (; i < vq; ++i) acc = acc + t[i];
+        s_part[tid] = acc;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (tid == 0) {
+        float s = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+        for (int i = 0; i < n - 4 * vq; ++i) s = s + s_tail[i];
+        float scale;
+        if (RMS) {  // graph.rs:141-156
+            const float inv_n = __fdiv_rn(1.0f, (float)n);
+            const float mean = s * inv_n;
+            const float var = mean + a.eps;
+            scale = __fdiv_rn(1.0f, sqrt_rn(var));
+        } else {    // graph.rs:182-193
+            const float var = s + a.eps;
+            scale = __fdiv_rn(1.0f, sqrt_rn(var));
+        }
+        s_scale = scale;
+    }
+    __syncthreads();
+    const float scale = s_scale;
+
+    if (a.q8.q) {
+        // quad per Q8_0 block (n % 32 == 0): 8 elements per lane
+        const int nb = n / 32;
+        const int part = tid & 3;
+        for (int blk = tid >> 2; blk < nb; blk += kNormThreads / 4) {
+            const int e0 = 32 * blk + 8 * part;
+            const float4 x0 = ld4(x + e0), x1 = ld4(x + e0 + 4);
+            float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            if (RMS) {
+                const float4 w0 = ld4(a.w + e0), w1 = ld4(a.w + e0 + 4);
+                const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float nx = v[k] * scale;
+                    v[k] = nx * wv[k];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = v[k] * scale;
+            }
+            if (a.out) {
+                float* o = a.out + (long)blockIdx.x * a.out_stride + e0;
+                *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+            store_q8_quad(a.q8, blockIdx.x, blk, part, make_float4(v[0], v[1], v[2], v[3]),
+                          make_float4(v[4], v[5], v[6], v[7]));
+        }
+    } else {
+        float* o = a.out + (long)blockIdx.x * a.out_stride;
+        for (int e = tid; e < n; e += kNormThreads) {
+            float y;
+            if (RMS) {
+                const float nx = x[e] * scale;
+                y = nx * a.w[e];
+            } else {
+                y = x[e] * scale;
+            }
+            o[e] = y;
+        }
+    }
+}
+
+// ---- SwiGLU: out[i] = silu(gate[i]) * up[i] over rows of n ----
+
+struct SwigluArgs {
+    const float* gate;  // [rows][n] contiguous
+    const float* up;
+    long total;         // rows * n
+    int n;
+    float* out;         // [rows][n] or nullptr
+    Q8Out q8;           // Q8_0 output, or q8.q == nullptr (then n % 32 == 0)
+};
+
+__global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
+#pragma clang fp contract(off)
+    if (a.q8.q) {
+        const long nblk = a.total / 32;
+        const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 2;
+        const int part = threadIdx.x & 3;
+        if (i >= nblk) return;  // uniform over the quad
+        const long e0 = i * 32 + 8 * part;
+        const float4 g0 = ld4(a.gate + e0), g1 = ld4(a.gate + e0 + 4);
+        const float4 u0 = ld4(a.up + e0), u1 = ld4(a.up + e0 + 4);
+        const float4 y0 = make_float4(jit_silu(g0.x) * u0.x, jit_silu(g0.y) * u0.y,
+                                      jit_silu(g0.z) * u0.z, jit_silu(g0.w) * u0.w);
+        const float4 y1 = make_float4(jit_silu(g1.x) * u1.x, jit_silu(g1.y) * u1.y,
+                                      jit_silu(g1.z) * u1.z, jit_silu(g1.w) * u1.w);
+        if (a.out) {
+            *reinterpret_cast<float4*>(a.out + e0) = y0;
+            *reinterpret_cast<float4*>(a.out + e0 + 4) = y1;
+        }
+        const int nb = a.n / 32;
+        const long row = i / nb;
+        store_q8_quad(a.q8, row, (int)(i - row * nb), part, y0, y1);
+        return;
+    }
+    for (long e = (long)blockIdx.x * blockDim.x + threadIdx.x; e < a.total;
+         e += (long)gridDim.x * blockDim.x)
+        a.out[e] = jit_silu(a.gate[e]) * a.up[e];
+}
+
+// ---- residual_add: out[i] = a[i] + b[i] ----
+
+__global__ __launch_bounds__(256) void add_kernel(const float* x, const float* y, long n,
+                                                  float* out) {
+    for (long e = (long)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+         e += (long)gridDim.x * blockDim.x)
+        out[e] = x[e] + y[e];
+}
+
+// ---- token embedding rows: dequantize_row_q4_0 of row tokens[t] ----
+// Thread per block: (q - 8) as f32 * d, low nibbles to elements 0..15 and
+// high nibbles to 16..31 (blocks.rs:85-99).
+
+__global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t* qs, const uint16_t* d,
+                                                         int d_stride, int nb, int vocab,
+                                                         const int32_t* tokens, int n,
+                                                         float* out, int* bad) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)n * nb) return;
+    const int t = (int)(i / nb), b = (int)(i - (long)t * nb);
+    const int tok = tokens[t];
+    float* o = out + (long)t * nb * 32 + 32 * b;
+    if (tok < 0 || tok >= vocab) {  // the host checks host-side ids; device ids are flagged
+        if (b == 0) atomicOr(bad, 1);
+        return;
+    }
+    const uint4 w = *reinterpret_cast<const uint4*>(qs + ((long)tok * nb + b) * 16);
+    const float sc = __half2float(__ushort_as_half(d[(long)tok * d_stride + b]));
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int byte = (wd[k] >> (8 * j)) & 0xFF;
+            lo[j] = (float)((byte & 0x0F) - 8) * sc;
+            hi[j] = (float)((byte >> 4) - 8) * sc;
+        }
+        *reinterpret_cast<float4*>(o + 4 * k) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<float4*>(o + 16 + 4 * k) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+    }
+}
+
+// ---- sample_argmax: the first index of the maximum ----
+// The reference scans in order with `val > best` from logits[0]: NaN never
+// wins after the first element, and a NaN first element wins outright.  In
+// parallel: each thread keeps its best non-NaN (value, index), ties go to the
+// lower index, and logits[0] being NaN short-cuts to 0.
+
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float v2, int i2) {
+    if (i2 < 0) return;
+    if (i < 0 || v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, int n,
+                                                                int32_t* out) {
+    __shared__ float s_v[kArgmaxThreads / 64];
+    __shared__ int s_i[kArgmaxThreads / 64];
+    float bv = 0.0f;
+    int bi = -1;
+    for (int e = threadIdx.x; e < n; e += kArgmaxThreads) {
+        const float v = x[e];
+        if (v != v) continue;
+        argmax_merge(bv, bi, v, e);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float v2 = __shfl_xor(bv, off);
+        const int i2 = __shfl_xor(bi, off);
+        argmax_merge(bv, bi, v2, i2);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_v[threadIdx.x >> 6] = bv;
+        s_i[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_merge(bv, bi, s_v[w], s_i[w]);
+        const float x0 = x[0];
+        out[0] = (x0 != x0 || bi < 0) ? 0 : bi;
+    }
+}
+
+template <bool RMS>
+hipError_t launch_norm_t(const NormArgs& a, int rows, hipStream_t st) {
+    const size_t lds = (size_t)4 * norm_sq_stride(a.n) * sizeof(float);
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(norm_rows_kernel<RMS>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(norm_rows_kernel<RMS>, dim3(rows), dim3(kNormThreads), lds, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int norm_max_n() { return 16384; }
+
+hipError_t launch_rmsnorm(const float* x, long x_stride, const float* w, int rows, int n,
+                          float eps, float* out, long out_stride, const Q8Out& q8,
+                          hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (n < 1 || n > norm_max_n() || (q8.q && n % 32) || (!q8.q && !out))
+        return hipErrorInvalidValue;
+    NormArgs a{x, x_stride, w, n, eps, out, out_stride, q8};
+    return w ? launch_norm_t<true>(a, rows, st) : launch_norm_t<false>(a, rows, st);
+}
+
+hipError_t launch_swiglu(const float* gate, const float* up, long total, int n, float* out,
+                         const Q8Out& q8, hipStream_t st) {
+    if (total <= 0) return hipSuccess;
+    if ((q8.q && (n <= 0 || n % 32 || total % n)) || (!q8.q && !out)) return hipErrorInvalidValue;
+    SwigluArgs a{gate, up, total, n, out, q8};
+    long grid;
+    if (q8.q) {
+        grid = (total / 32 + 63) / 64;
+    } else {
+        grid = (total + 255) / 256;
+        if (grid > 65536) grid = 65536;
+    }
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(const float* x, const float* y, long n, float* out, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    long grid = (n + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, y, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const uint8_t* qs, const uint16_t* d, int nb, int vocab,
+                             const int32_t* tokens, int n, float* out, int* bad,
+                             hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const long threads = (long)n * nb;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       st, qs, d, q4_scale_stride(nb), nb, vocab, tokens, n, out, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* x, int n, int32_t* out, hipStream_t st) {
+    if (n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, st, x, n, out);
+    return hipGetLastError();
+}
+
+}  // namespace slm

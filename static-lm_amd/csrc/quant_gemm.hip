@@ -26,57 +26,13 @@
 #include <stdint.h>
 
 #include "attn_common.h"
+#include "quant_common.h"
 #include "slm_internal.h"
 
 namespace slm {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
-
-// `(x * id).round().clamp(-127.0, 127.0) as i8`: round half away from zero,
-// clamp keeps NaN, the cast sends NaN to 0.
-__device__ __forceinline__ int q8_value(float v) {
-    float r = roundf(v);
-    r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
-    return r != r ? 0 : (int)r;
-}
-
-// Four consecutive lanes quantize one block: lane part p holds elements
-// 8p..8p+7; returns them packed (2 dwords), with the block's f16 scale and
-// the sum of its 32 quantized values in every lane of the quad.
-__device__ __forceinline__ void quantize_q8_quad(const float4 f0, const float4 f1, uint2* q,
-                                                 uint16_t* dbits, int* sum) {
-#pragma clang fp contract(off)
-    const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float av = fabsf(v[i]);
-        amax = av > amax ? av : amax;
-    }
-    float o = dpp<0xB1>(amax);  // quad_perm [1,0,3,2]
-    amax = o > amax ? o : amax;
-    o = dpp<0x4E>(amax);        // quad_perm [2,3,0,1]
-    amax = o > amax ? o : amax;
-    const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    int s = 0;
-    uint32_t w[2] = {0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int qv = q8_value(v[i] * id);
-        s += qv;
-        w[i >> 2] |= (uint32_t)(qv & 0xFF) << (8 * (i & 3));
-    }
-    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
-    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
-    *q = make_uint2(w[0], w[1]);
-    *dbits = f2h(d);
-    *sum = s;
-}
 
 // ---- standalone quantize_row_q8_0: 34-byte BlockQ8_0 output ----
 // Four lanes per block (coalesced 32-byte reads per lane).

@@ -10,59 +10,9 @@
 #include <string>
 #include <vector>
 
-#include "slm_internal.h"
+#include "slm_host.h"
 
-// A Q4_0 weight matrix on one device: nibbles [rows][cols/32][16] and f16
-// scales [rows][cols/32 rounded up to 8], repacked from 18-byte BlockQ4_0
-// (blocks.rs:11-19).
-struct slm_q4_matrix {
-    int device = 0;
-    int rows = 0;
-    int cols = 0;
-    uint8_t* qs = nullptr;
-    uint16_t* d = nullptr;
-};
-
-struct slm_attn_ctx {
-    slm_attn_config cfg{};
-    slm::Shape shape{};
-    int device = 0;
-    hipStream_t own_stream = nullptr;
-    hipStream_t stream = nullptr;
-    // [num_layers][2][max_seq_len][kv_dim] f32, the arena's KV slices in order
-    float* kv = nullptr;
-    size_t kv_floats = 0;
-    // RoPE tables [max_seq_len][head_dim/2]
-    float* cos_t = nullptr;
-    float* sin_t = nullptr;
-    // split-K partials of one decode row
-    float* part_o = nullptr;
-    float* part_ml = nullptr;
-    int max_splits = 1;
-    // staging for the host-pointer entry points
-    float* stage = nullptr;
-    size_t stage_floats = 0;
-    // projections: Q8_0 activations (i8 [blocks][32], f32 scales) and the
-    // q | k | v rows the GEMMs produce for the attention kernels
-    uint32_t* q8_q = nullptr;
-    float* q8_d = nullptr;
-    size_t q8_blocks = 0;
-    float* qkv = nullptr;
-    size_t qkv_floats = 0;
-    // kernel timing
-    bool profiling = false;
-    struct Pending {
-        int kind;
-        hipEvent_t begin;
-        hipEvent_t end;
-    };
-    std::vector<Pending> pending;
-    std::vector<hipEvent_t> spare_events;
-    slm_kernel_stat stats[SLM_K_COUNT]{};
-    std::string err;
-};
-
-namespace {
+namespace slm_host {
 
 thread_local std::string g_last_error;
 
@@ -77,11 +27,6 @@ int hip_fail(slm_attn_ctx* c, hipError_t e, const char* what) {
                 std::string(what) + ": " + hipGetErrorString(e));
 }
 
-#define SLM_HIP(c, expr)                                   \
-    do {                                                   \
-        hipError_t e_ = (expr);                            \
-        if (e_ != hipSuccess) return hip_fail(c, e_, #expr); \
-    } while (0)
 
 // LayerWorkspace::allocate asserts (transformer.rs:81-101).
 int validate(const slm_attn_config* cfg, std::string* why) {
@@ -175,34 +120,6 @@ hipEvent_t take_event(slm_attn_ctx* c) {
     return e;
 }
 
-// Brackets one kernel launch with events while profiling is on.
-struct Timed {
-    slm_attn_ctx* c;
-    int kind;
-    hipEvent_t b = nullptr;
-    hipEvent_t e = nullptr;
-    Timed(slm_attn_ctx* ctx, int k) : c(ctx), kind(k) {
-        if (!c->profiling) return;
-        b = take_event(c);
-        e = take_event(c);
-        if (b && e && hipEventRecord(b, c->stream) != hipSuccess) drop();
-    }
-    void done() {
-        if (!b || !e) return;
-        if (hipEventRecord(e, c->stream) != hipSuccess) {
-            drop();
-            return;
-        }
-        c->pending.push_back({kind, b, e});
-        b = e = nullptr;
-    }
-    // A launch whose events could not be recorded is left out of the stats.
-    void drop() {
-        if (b) c->spare_events.push_back(b);
-        if (e) c->spare_events.push_back(e);
-        b = e = nullptr;
-    }
-};
 
 float* k_base(slm_attn_ctx* c, int layer) {
     return c->kv + (size_t)(2 * layer) * c->cfg.max_seq_len * c->shape.kv_dim;
@@ -330,30 +247,17 @@ int ensure_stage(slm_attn_ctx* c, size_t floats) {
     return SLM_OK;
 }
 
-// Grows a device buffer (after the stream drained its users).
-template <class T>
-int ensure_buffer(slm_attn_ctx* c, T** buf, size_t* have, size_t want, const char* what) {
-    if (*have >= want) return SLM_OK;
-    if (*buf) {
-        SLM_HIP(c, hipStreamSynchronize(c->stream));
-        SLM_HIP(c, hipFree(*buf));
-        *buf = nullptr;
-        *have = 0;
-    }
-    hipError_t e = hipMalloc(buf, want * sizeof(T));
-    if (e != hipSuccess) return hip_fail(c, e, what);
-    *have = want;
-    return SLM_OK;
-}
 
 // Q8_0 activations of n rows of nb blocks: i8 [n][nb][32] and f32 scales
 // [n][q4_scale_stride(nb)].
 int ensure_q8(slm_attn_ctx* c, size_t n, int nb) {
     const size_t blocks = n * (size_t)slm::q4_scale_stride(nb);  // covers both
-    size_t have_q = c->q8_blocks * 8, have_d = c->q8_blocks;
+    size_t have_q = c->q8_blocks * 8, have_d = c->q8_blocks, have_s = c->q8_blocks;
     int rc = ensure_buffer(c, &c->q8_q, &have_q, blocks * 8, "hipMalloc(q8 activations)");
     if (rc) return rc;
     rc = ensure_buffer(c, &c->q8_d, &have_d, blocks, "hipMalloc(q8 scales)");
+    if (rc) return rc;
+    rc = ensure_buffer(c, &c->q8_s, &have_s, blocks, "hipMalloc(q8 sums)");
     if (rc) return rc;
     if (blocks > c->q8_blocks) c->q8_blocks = blocks;
     return SLM_OK;
@@ -368,7 +272,7 @@ int check_matrix(slm_attn_ctx* c, const slm_q4_matrix* m, int rows, int cols, co
     return SLM_OK;
 }
 
-slm::Q4Job q4_job(const slm_q4_matrix* m, float* out, const float* res = nullptr) {
+slm::Q4Job q4_job(const slm_q4_matrix* m, float* out, const float* res) {
     return slm::Q4Job{m->qs, m->d, out, m->rows, m->rows, res};
 }
 
@@ -472,7 +376,9 @@ int project_qkv(slm_attn_ctx* c, int n, const float* xb, const slm_q4_matrix* wq
     return launch_status(c, e, "q4 gemm kernel launch");
 }
 
-}  // namespace
+}  // namespace slm_host
+
+using namespace slm_host;
 
 extern "C" {
 
@@ -528,7 +434,10 @@ int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
         slm_attn_destroy(c);
         return code;
     };
-    e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    // A blocking stream: ordered with the legacy default stream, so device
+    // buffers the caller fills there are ready before the context's kernels
+    // read them, and its results before default-stream work reads them.
+    e = hipStreamCreateWithFlags(&c->own_stream, hipStreamDefault);
     if (e != hipSuccess) return bail(hip_fail(nullptr, e, "hipStreamCreate"));
     c->stream = c->own_stream;
 
@@ -587,7 +496,11 @@ void slm_attn_destroy(slm_attn_ctx* c) {
     (void)hipFree(c->stage);
     (void)hipFree(c->q8_q);
     (void)hipFree(c->q8_d);
+    (void)hipFree(c->q8_s);
     (void)hipFree(c->qkv);
+    (void)hipFree(c->blk_att);
+    (void)hipFree(c->blk_mid);
+    (void)hipFree(c->blk_hid);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }

@@ -107,8 +107,38 @@ hipError_t launch_q4_gemv(const Q4Job* jobs, int njobs, const float* x, int nb, 
 // [nb]); nb at most 512
 hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
                              const int* as, int nb, hipStream_t st);
+// Q8_0 blocks of a row-major [rows][nb * 32] activation, as the projections
+// read them: q [rows][nb][8] (32 i8 per block), d and the blocks' sums of
+// quantized values [rows][d_stride] (s may be nullptr; the GEMM needs none).
+struct Q8Out {
+    uint32_t* q;
+    float* d;
+    int* s;
+    int nb;
+    int d_stride;
+};
 // any batch, from pre-quantized activations
 hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
                           int nb, int batch, hipStream_t st);
+
+// JIT kernels (norm_act.hip).  RMSNorm (w != nullptr) or L2 norm (w ==
+// nullptr) of `rows` rows of n, into out (f32) and/or q8 (n % 32 == 0).
+int norm_max_n();
+hipError_t launch_rmsnorm(const float* x, long x_stride, const float* w, int rows, int n,
+                          float eps, float* out, long out_stride, const Q8Out& q8,
+                          hipStream_t st);
+// out = silu(gate) * up over `total` elements, into out and/or q8 (rows of
+// n elements, n % 32 == 0; n is only read for q8)
+hipError_t launch_swiglu(const float* gate, const float* up, long total, int n, float* out,
+                         const Q8Out& q8, hipStream_t st);
+// out = x + y
+hipError_t launch_add(const float* x, const float* y, long n, float* out, hipStream_t st);
+// rows tokens[0..n) of a Q4_0 matrix dequantized into out [n][nb*32]; a
+// device-side token id outside [0, vocab) sets *bad and leaves its row
+hipError_t launch_embed_rows(const uint8_t* qs, const uint16_t* d, int nb, int vocab,
+                             const int32_t* tokens, int n, float* out, int* bad,
+                             hipStream_t st);
+// first index of the maximum of x[0..n) (sample_argmax)
+hipError_t launch_argmax(const float* x, int n, int32_t* out, hipStream_t st);
 
 }  // namespace slm
