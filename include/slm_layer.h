@@ -73,6 +73,54 @@ typedef struct slm_layer_weights {
 int slm_layer_forward_dev(slm_attn_ctx* ctx, int32_t layer, int32_t start, int32_t n,
                           const slm_layer_weights* w, float rms_eps, float* x);
 
+/* ---- the whole model (TransformerModel, transformer.rs:699-957) ---- */
+
+/* A token id outside [0, vocab_size) (transformer.rs:757-760, 813, 911). */
+#define SLM_ERR_TOKEN (-11)
+
+/* ModelWeights (transformer.rs:49-56) on the context's device: one
+ * slm_layer_weights per layer of the context (a host array), the final
+ * RMSNorm scale (device [dim]) and the vocab_size x dim token embedding and
+ * lm_head matrices. */
+typedef struct slm_model_weights {
+    const slm_q4_matrix* token_embd;
+    const slm_layer_weights* layers;  /* [num_layers] */
+    int32_t num_layers;
+    const float* output_norm;
+    const slm_q4_matrix* lm_head;
+} slm_model_weights;
+
+/* TransformerModel::forward_token (transformer.rs:746-796): the embedding row
+ * of `token` (dequantize_row_q4_0), every layer at `pos`, the final RMSNorm,
+ * the lm_head projection into logits and the greedy argmax (sample_argmax,
+ * :654-666: the first index of the maximum).  logits is a device [vocab]
+ * buffer or NULL (then the context keeps them); *next_token is written on the
+ * host, so the call waits for the stream. */
+int slm_model_forward_token_dev(slm_attn_ctx* ctx, const slm_model_weights* w, float rms_eps,
+                                int32_t token, int32_t pos, float* logits, int32_t* next_token);
+
+/* TransformerModel::prefill_tokens (transformer.rs:800-850): the n host token
+ * ids at rows start..start+n-1 through every layer as one batch, then the
+ * logits and argmax of the last row. */
+int slm_model_prefill_dev(slm_attn_ctx* ctx, const slm_model_weights* w, float rms_eps,
+                          const int32_t* tokens, int32_t n, int32_t start, float* logits,
+                          int32_t* next_token);
+
+/* TransformerModel::generate (transformer.rs:853-899): prefill of the prompt
+ * at 0, then greedy decode, writing up to max_out tokens to out_tokens (host)
+ * and stopping after `eos` (eos < 0: none) or at max_seq_len.  *n_out is the
+ * number written (0 for an empty prompt or max_out == 0). */
+int slm_model_generate_dev(slm_attn_ctx* ctx, const slm_model_weights* w, float rms_eps,
+                           const int32_t* prompt, int32_t n_prompt, int32_t* out_tokens,
+                           int32_t max_out, int32_t eos, int32_t* n_out);
+
+/* TransformerModel::embed_tokens (transformer.rs:904-957): the n tokens
+ * through every layer as a batch at 0, each row normed with output_norm, the
+ * rows averaged (accum += row * (1/n) in order) and L2-normalized into out
+ * (device [dim]). */
+int slm_model_embed_dev(slm_attn_ctx* ctx, const slm_model_weights* w, float rms_eps,
+                        const int32_t* tokens, int32_t n, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -445,3 +445,80 @@ class LayerWeights:
         return OrcLayerWeights(_p(self.rms_att), _u8(self.wq), _u8(self.wk), _u8(self.wv),
                                _u8(self.wo), _p(self.rms_ffn), _u8(self.w_gate),
                                _u8(self.w_up), _u8(self.w_down))
+
+
+# ---- the whole model (TransformerModel, transformer.rs:699-957) ----
+
+def sample_argmax(logits) -> int:
+    """sample_argmax (transformer.rs:655-667): scan from index 0 with a
+    strict `>`, so the first maximum wins and a later NaN never does."""
+    logits = _f32(logits)
+    best, val = 0, logits[0]
+    for i in range(1, logits.size):
+        if logits[i] > val:
+            best, val = i, logits[i]
+    return best
+
+
+@dataclass
+class ModelWeights:
+    """ModelWeights (transformer.rs:49-56): BlockQ4_0 token_embd and lm_head
+    [vocab][dim], per-layer LayerWeights, f32 output_norm."""
+    token_embd: np.ndarray
+    layers: list
+    output_norm: np.ndarray
+    lm_head: np.ndarray
+    vocab_size: int
+
+
+def embed_rows(token_embd: np.ndarray, tokens, dim: int) -> np.ndarray:
+    """dequantize_row_q4_0 of each token's row (transformer.rs:769-770)."""
+    nb = dim // QK
+    blocks = np.ascontiguousarray(token_embd).reshape(-1, Q4_BYTES)
+    return np.stack([dequantize_q4_0(blocks[t * nb:(t + 1) * nb]) for t in tokens])
+
+
+def model_forward(om: "OracleModel", w: ModelWeights, eps: float, tokens, start: int):
+    """forward_token (n = 1, transformer.rs:746-796) / prefill_tokens (n > 1,
+    :800-850): returns (logits of the last row, argmax, residual rows)."""
+    dim = om.cfg.dim
+    x = embed_rows(w.token_embd, tokens, dim)
+    for layer, lw in enumerate(w.layers):
+        x = om.layer_forward(layer, start, x, lw, eps)
+    xb = jit_rmsnorm(x[-1], w.output_norm, eps)
+    logits = gemm_q4_0_f32(w.lm_head, xb, 1, w.vocab_size, dim)[0]
+    return logits, sample_argmax(logits), x
+
+
+def model_generate(om: "OracleModel", w: ModelWeights, eps: float, prompt, max_out: int,
+                   eos: int = -1) -> list:
+    """generate (transformer.rs:853-899)."""
+    if max_out <= 0 or len(prompt) == 0:
+        return []
+    _, nxt, _ = model_forward(om, w, eps, prompt, 0)
+    out = [nxt]
+    if nxt == eos:
+        return out
+    pos = len(prompt)
+    while len(out) < max_out and pos < om.cfg.max_seq_len:
+        _, nxt, _ = model_forward(om, w, eps, [nxt], pos)
+        out.append(nxt)
+        pos += 1
+        if nxt == eos:
+            break
+    return out
+
+
+def model_embed(om: "OracleModel", w: ModelWeights, eps: float, tokens) -> np.ndarray:
+    """embed_tokens (transformer.rs:904-957): the batch at 0 through every
+    layer, each row normed with output_norm, accum += row * (1/n) in order,
+    then the L2 norm."""
+    dim = om.cfg.dim
+    x = embed_rows(w.token_embd, tokens, dim)
+    for layer, lw in enumerate(w.layers):
+        x = om.layer_forward(layer, 0, x, lw, eps)
+    inv = np.float32(1.0) / np.float32(len(tokens))
+    acc = np.zeros(dim, np.float32)
+    for b in range(len(tokens)):
+        acc = acc + jit_rmsnorm(x[b], w.output_norm, eps) * inv
+    return jit_l2_norm(acc, eps)

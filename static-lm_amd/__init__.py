@@ -40,9 +40,10 @@ ERRORS = {
     -8: "SLM_ERR_UNSUPPORTED",
     -9: "SLM_ERR_DEVICE",
     -10: "SLM_ERR_SHAPE",
+    -11: "SLM_ERR_TOKEN",
 }
 (ERR_CONFIG, ERR_POS, ERR_BATCH, ERR_LAYER, ERR_ALIAS, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED,
- ERR_DEVICE, ERR_SHAPE) = (-1, -2, -3, -4, -5, -6, -7, -8, -9, -10)
+ ERR_DEVICE, ERR_SHAPE, ERR_TOKEN) = (-1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11)
 
 KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope", "quant", "gemm", "norm",
                 "elem")
@@ -144,6 +145,10 @@ SIGNATURES = {
     "slm_swiglu_dev": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P]),
     "slm_residual_add_dev": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P]),
     "slm_layer_forward_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, ctypes.c_float, _P]),
+    "slm_model_forward_token_dev": (ctypes.c_int, [_P, _P, ctypes.c_float, _I, _I, _P, _P]),
+    "slm_model_prefill_dev": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _I, _I, _P, _P]),
+    "slm_model_generate_dev": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _I, _P, _I, _I, _P]),
+    "slm_model_embed_dev": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _I, _P]),
 }
 
 
@@ -151,6 +156,12 @@ class LayerWeightsC(ctypes.Structure):
     """slm_layer_weights (include/slm_layer.h)."""
     _fields_ = [("rms_att", _P), ("wq", _P), ("wk", _P), ("wv", _P), ("wo", _P),
                 ("rms_ffn", _P), ("w_gate", _P), ("w_up", _P), ("w_down", _P)]
+
+
+class ModelWeightsC(ctypes.Structure):
+    """slm_model_weights (include/slm_layer.h)."""
+    _fields_ = [("token_embd", _P), ("layers", ctypes.POINTER(LayerWeightsC)),
+                ("num_layers", ctypes.c_int32), ("output_norm", _P), ("lm_head", _P)]
 
 _lib = None
 
@@ -342,6 +353,43 @@ class AttentionContext:
         self._check(self.lib.slm_layer_forward_dev(self._h, layer, start, n, ctypes.byref(c),
                                                    rms_eps, x))
 
+    # -- the whole model (TransformerModel) ---------------------------------------
+    def model_forward_token_dev(self, weights: "ModelWeights", rms_eps: float, token: int,
+                                pos: int, logits=0) -> int:
+        nxt = ctypes.c_int32()
+        c = weights.c()
+        self._check(self.lib.slm_model_forward_token_dev(self._h, ctypes.byref(c), rms_eps,
+                                                         token, pos, logits or None,
+                                                         ctypes.byref(nxt)))
+        return nxt.value
+
+    def model_prefill_dev(self, weights: "ModelWeights", rms_eps: float, tokens, start: int = 0,
+                          logits=0) -> int:
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        nxt = ctypes.c_int32()
+        c = weights.c()
+        self._check(self.lib.slm_model_prefill_dev(self._h, ctypes.byref(c), rms_eps,
+                                                   toks.ctypes.data, toks.size, start,
+                                                   logits or None, ctypes.byref(nxt)))
+        return nxt.value
+
+    def model_generate_dev(self, weights: "ModelWeights", rms_eps: float, prompt, max_out: int,
+                           eos: int = -1) -> list[int]:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max(max_out, 1), np.int32)
+        n = ctypes.c_int32()
+        c = weights.c()
+        self._check(self.lib.slm_model_generate_dev(self._h, ctypes.byref(c), rms_eps,
+                                                    p.ctypes.data, p.size, out.ctypes.data,
+                                                    max_out, eos, ctypes.byref(n)))
+        return [int(t) for t in out[:n.value]]
+
+    def model_embed_dev(self, weights: "ModelWeights", rms_eps: float, tokens, out) -> None:
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        c = weights.c()
+        self._check(self.lib.slm_model_embed_dev(self._h, ctypes.byref(c), rms_eps,
+                                                 toks.ctypes.data, toks.size, out))
+
     # -- streams, cache access, timing ------------------------------------------
     def set_stream(self, stream: int | None) -> None:
         self._check(self.lib.slm_attn_set_stream(self._h, stream or None))
@@ -450,6 +498,21 @@ class LayerWeights:
     def close(self) -> None:
         for m in self.mats:
             m.close()
+
+
+class ModelWeights:
+    """slm_model_weights (include/slm_layer.h): per-layer LayerWeights, the
+    token embedding and lm_head Q4Matrix, and the final RMSNorm scale as a
+    device pointer the caller keeps alive."""
+
+    def __init__(self, token_embd: Q4Matrix, layers: list, output_norm: int, lm_head: Q4Matrix):
+        self.token_embd, self.layers = token_embd, list(layers)
+        self.output_norm, self.lm_head = output_norm, lm_head
+        self._arr = (LayerWeightsC * len(self.layers))(*[lw.c() for lw in self.layers])
+
+    def c(self) -> ModelWeightsC:
+        return ModelWeightsC(self.token_embd.handle, self._arr, len(self.layers),
+                             self.output_norm, self.lm_head.handle)
 
 
 def header_functions(*headers: os.PathLike | str) -> list[str]:

@@ -264,6 +264,23 @@ __global__ __launch_bounds__(256) void add_kernel(const float* x, const float* y
         out[e] = x[e] + y[e];
 }
 
+// ---- mean pool of embed_tokens (transformer.rs:934-950) ----
+// accum starts at 0 and takes accum[i] += normed_b[i] * inv_batch for b in
+// order: a product then a sum per row, thread per element.
+
+__global__ __launch_bounds__(256) void mean_pool_kernel(const float* rows, int n, int dim,
+                                                        float inv, float* out) {
+#pragma clang fp contract(off)
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= dim) return;
+    float acc = 0.0f;
+    for (int b = 0; b < n; ++b) {
+        const float t = rows[(long)b * dim + i] * inv;
+        acc = acc + t;
+    }
+    out[i] = acc;
+}
+
 // ---- token embedding rows: dequantize_row_q4_0 of row tokens[t] ----
 // Thread per block: (q - 8) as f32 * d, low nibbles to elements 0..15 and
 // high nibbles to 16..31 (blocks.rs:85-99).
@@ -401,6 +418,14 @@ hipError_t launch_embed_rows(const uint8_t* qs, const uint16_t* d, int nb, int v
     const long threads = (long)n * nb;
     hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        st, qs, d, q4_scale_stride(nb), nb, vocab, tokens, n, out, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_mean_pool(const float* rows, int n, int dim, float inv, float* out,
+                            hipStream_t st) {
+    if (n <= 0 || dim <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mean_pool_kernel, dim3((dim + 255) / 256), dim3(256), 0, st, rows, n, dim,
+                       inv, out);
     return hipGetLastError();
 }
 

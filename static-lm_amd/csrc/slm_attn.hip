@@ -501,6 +501,10 @@ void slm_attn_destroy(slm_attn_ctx* c) {
     (void)hipFree(c->blk_att);
     (void)hipFree(c->blk_mid);
     (void)hipFree(c->blk_hid);
+    (void)hipFree(c->mdl_x);
+    (void)hipFree(c->mdl_tok);
+    (void)hipFree(c->mdl_logits);
+    (void)hipFree(c->mdl_flags);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }

@@ -61,6 +61,16 @@ struct slm_attn_ctx {
     size_t blk_mid_floats = 0;
     float* blk_hid = nullptr;
     size_t blk_hid_floats = 0;
+    // whole-model workspace (slm_layer.h): residual rows [msl][dim], token
+    // ids [msl], logits [vocab], the argmax result and a token-range flag
+    float* mdl_x = nullptr;
+    size_t mdl_x_floats = 0;
+    int32_t* mdl_tok = nullptr;
+    size_t mdl_tok_n = 0;
+    float* mdl_logits = nullptr;
+    size_t mdl_logits_n = 0;
+    int32_t* mdl_flags = nullptr;  // [0] argmax, [1] bad token
+    size_t mdl_flags_n = 0;
     // kernel timing
     bool profiling = false;
     struct Pending {

@@ -138,6 +138,9 @@ hipError_t launch_add(const float* x, const float* y, long n, float* out, hipStr
 hipError_t launch_embed_rows(const uint8_t* qs, const uint16_t* d, int nb, int vocab,
                              const int32_t* tokens, int n, float* out, int* bad,
                              hipStream_t st);
+// out[i] = sum over b in order of rows[b][i] * inv (embed_tokens' pooling)
+hipError_t launch_mean_pool(const float* rows, int n, int dim, float inv, float* out,
+                            hipStream_t st);
 // first index of the maximum of x[0..n) (sample_argmax)
 hipError_t launch_argmax(const float* x, int n, int32_t* out, hipStream_t st);
 

@@ -210,3 +210,215 @@ int slm_layer_forward_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t
 }
 
 }  // extern "C"
+
+// ---- the whole model ----
+
+namespace {
+
+int check_model(slm_attn_ctx* c, const slm_model_weights* w, int* vocab) {
+    const slm::Shape& s = c->shape;
+    if (!w || !w->layers) return fail(c, SLM_ERR_ARG, "weights is NULL");
+    if (w->num_layers != c->cfg.num_layers)
+        return fail(c, SLM_ERR_CONFIG, "layer count mismatch");  // transformer.rs:762-766
+    int rc;
+    if (!w->token_embd) return fail(c, SLM_ERR_ARG, "token_embd is NULL");
+    const int v = w->token_embd->rows;
+    if ((rc = check_matrix(c, w->token_embd, v, s.dim, "token_embd")) ||
+        (rc = check_matrix(c, w->lm_head, v, s.dim, "lm_head")) ||
+        (rc = check_dev_ptrs(c, {w->output_norm})))
+        return rc;
+    *vocab = v;
+    return SLM_OK;
+}
+
+int ensure_model(slm_attn_ctx* c, int rows, int vocab) {
+    int rc;
+    if ((rc = ensure_buffer(c, &c->mdl_x, &c->mdl_x_floats, (size_t)rows * c->shape.dim,
+                            "hipMalloc(model rows)")) ||
+        (rc = ensure_buffer(c, &c->mdl_tok, &c->mdl_tok_n, (size_t)rows, "hipMalloc(tokens)")) ||
+        (rc = ensure_buffer(c, &c->mdl_logits, &c->mdl_logits_n, (size_t)vocab,
+                            "hipMalloc(logits)")) ||
+        (rc = ensure_buffer(c, &c->mdl_flags, &c->mdl_flags_n, 2, "hipMalloc(flags)")))
+        return rc;
+    return SLM_OK;
+}
+
+int check_tokens(slm_attn_ctx* c, const int32_t* tokens, int n, int vocab) {
+    if (!tokens) return fail(c, SLM_ERR_ARG, "tokens is NULL");
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= vocab)
+            return fail(c, SLM_ERR_TOKEN, "token_id out of vocabulary bounds");
+    return SLM_OK;
+}
+
+// Embedding rows of n host tokens into the model rows [0, n).
+int embed(slm_attn_ctx* c, const slm_model_weights* w, const int32_t* tokens, int n, int vocab) {
+    SLM_HIP(c, hipMemcpyAsync(c->mdl_tok, tokens, (size_t)n * sizeof(int32_t),
+                              hipMemcpyHostToDevice, c->stream));
+    Timed t(c, SLM_K_ELEM);
+    hipError_t e = slm::launch_embed_rows(w->token_embd->qs, w->token_embd->d, c->shape.dim / 32,
+                                          vocab, c->mdl_tok, n, c->mdl_x, c->mdl_flags + 1,
+                                          c->stream);
+    t.done();
+    return launch_status(c, e, "embedding kernel launch");
+}
+
+int all_layers(slm_attn_ctx* c, const slm_model_weights* w, float eps, int start, int n) {
+    for (int l = 0; l < w->num_layers; ++l) {
+        const int rc = slm_layer_forward_dev(c, l, start, n, &w->layers[l], eps, c->mdl_x);
+        if (rc) return rc;
+    }
+    return SLM_OK;
+}
+
+// Final RMSNorm of model row `row`, lm_head, argmax; *next on the host.
+int head(slm_attn_ctx* c, const slm_model_weights* w, float eps, int row, int vocab,
+         float* logits, int32_t* next) {
+    const slm::Shape& s = c->shape;
+    const int nb = s.dim / 32;
+    float* lg = logits ? logits : c->mdl_logits;
+    int rc;
+    if ((rc = ensure_q8(c, 1, nb))) return rc;
+    {
+        Timed t(c, SLM_K_NORM);
+        hipError_t e = slm::launch_rmsnorm(c->mdl_x + (size_t)row * s.dim, s.dim, w->output_norm,
+                                           1, s.dim, eps, nullptr, 0, q8_out(c, nb), c->stream);
+        t.done();
+        if ((rc = run(c, e, "rmsnorm kernel launch"))) return rc;
+    }
+    {
+        const slm::Q4Job job = q4_job(w->lm_head, lg);
+        Timed t(c, SLM_K_GEMM);
+        hipError_t e = slm::launch_q4_gemv_q8(&job, 1, c->q8_q, c->q8_d, c->q8_s, nb, c->stream);
+        t.done();
+        if ((rc = run(c, e, "q4 projection kernel launch"))) return rc;
+    }
+    {
+        Timed t(c, SLM_K_ELEM);
+        hipError_t e = slm::launch_argmax(lg, vocab, c->mdl_flags, c->stream);
+        t.done();
+        if ((rc = run(c, e, "argmax kernel launch"))) return rc;
+    }
+    int32_t h[2] = {0, 0};
+    SLM_HIP(c, hipMemcpyAsync(h, c->mdl_flags, sizeof h, hipMemcpyDeviceToHost, c->stream));
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
+    if (h[1]) return fail(c, SLM_ERR_TOKEN, "token_id out of vocabulary bounds");
+    *next = h[0];
+    return SLM_OK;
+}
+
+int model_prefill(slm_attn_ctx* c, const slm_model_weights* w, float eps, const int32_t* tokens,
+                  int n, int start, float* logits, int32_t* next) {
+    int rc, vocab = 0;
+    if ((rc = check_model(c, w, &vocab)) || (rc = check_batch(c, start, n))) return rc;
+    if (!next) return fail(c, SLM_ERR_ARG, "next_token is NULL");
+    if ((rc = check_tokens(c, tokens, n, vocab)) || (rc = ensure_model(c, n, vocab))) return rc;
+    if (logits && ((rc = check_dev_ptrs(c, {logits})) ||
+                   (rc = check_io(c, logits, (size_t)vocab, {}))))
+        return rc;
+    SLM_HIP(c, hipMemsetAsync(c->mdl_flags, 0, 2 * sizeof(int32_t), c->stream));
+    if ((rc = embed(c, w, tokens, n, vocab)) || (rc = all_layers(c, w, eps, start, n)))
+        return rc;
+    return head(c, w, eps, n - 1, vocab, logits, next);
+}
+
+}  // namespace
+
+extern "C" {
+
+int slm_model_forward_token_dev(slm_attn_ctx* c, const slm_model_weights* w, float rms_eps,
+                                int32_t token, int32_t pos, float* logits, int32_t* next_token) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    int rc;
+    if ((rc = check_pos(c, pos))) return rc;
+    return model_prefill(c, w, rms_eps, &token, 1, pos, logits, next_token);
+}
+
+int slm_model_prefill_dev(slm_attn_ctx* c, const slm_model_weights* w, float rms_eps,
+                          const int32_t* tokens, int32_t n, int32_t start, float* logits,
+                          int32_t* next_token) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    return model_prefill(c, w, rms_eps, tokens, n, start, logits, next_token);
+}
+
+int slm_model_generate_dev(slm_attn_ctx* c, const slm_model_weights* w, float rms_eps,
+                           const int32_t* prompt, int32_t n_prompt, int32_t* out_tokens,
+                           int32_t max_out, int32_t eos, int32_t* n_out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (!n_out) return fail(c, SLM_ERR_ARG, "n_out is NULL");
+    *n_out = 0;
+    if (max_out <= 0 || n_prompt <= 0) return SLM_OK;  // transformer.rs:862-864
+    if (!out_tokens) return fail(c, SLM_ERR_ARG, "out_tokens is NULL");
+    if (n_prompt > c->cfg.max_seq_len)  // :866
+        return fail(c, SLM_ERR_BATCH, "prompt longer than max_seq_len");
+    int32_t next = 0;
+    int rc = model_prefill(c, w, rms_eps, prompt, n_prompt, 0, nullptr, &next);
+    if (rc) return rc;
+    out_tokens[0] = next;
+    int generated = 1;
+    if (eos >= 0 && next == eos) {
+        *n_out = generated;
+        return SLM_OK;
+    }
+    for (int pos = n_prompt; generated < max_out && pos < c->cfg.max_seq_len; ++pos) {
+        if ((rc = model_prefill(c, w, rms_eps, &next, 1, pos, nullptr, &next))) {
+            *n_out = generated;
+            return rc;
+        }
+        out_tokens[generated++] = next;
+        if (eos >= 0 && next == eos) break;
+    }
+    *n_out = generated;
+    return SLM_OK;
+}
+
+int slm_model_embed_dev(slm_attn_ctx* c, const slm_model_weights* w, float rms_eps,
+                        const int32_t* tokens, int32_t n, float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    const slm::Shape& s = c->shape;
+    int rc, vocab = 0;
+    if ((rc = check_model(c, w, &vocab)) || (rc = check_batch(c, 0, n)) ||
+        (rc = check_tokens(c, tokens, n, vocab)) || (rc = ensure_model(c, n, vocab)) ||
+        (rc = check_dev_ptrs(c, {out})) || (rc = check_io(c, out, (size_t)s.dim, {})))
+        return rc;
+    // normed rows reuse the block's attention-row buffer (free after the layers)
+    if ((rc = ensure_buffer(c, &c->blk_att, &c->blk_att_floats, (size_t)n * s.dim,
+                            "hipMalloc(block rows)")))
+        return rc;
+    SLM_HIP(c, hipMemsetAsync(c->mdl_flags, 0, 2 * sizeof(int32_t), c->stream));
+    if ((rc = embed(c, w, tokens, n, vocab)) || (rc = all_layers(c, w, rms_eps, 0, n))) return rc;
+    hipError_t e;
+    {
+        Timed t(c, SLM_K_NORM);
+        e = slm::launch_rmsnorm(c->mdl_x, s.dim, w->output_norm, n, s.dim, rms_eps, c->blk_att,
+                                s.dim, slm::Q8Out{}, c->stream);
+        t.done();
+        if ((rc = run(c, e, "rmsnorm kernel launch"))) return rc;
+    }
+    // accum (the block's x_mid buffer, [dim] at least) then its L2 norm
+    if ((rc = ensure_buffer(c, &c->blk_mid, &c->blk_mid_floats, (size_t)s.dim,
+                            "hipMalloc(block rows)")))
+        return rc;
+    float* accum = c->blk_mid;
+    {
+        Timed t(c, SLM_K_ELEM);
+        e = slm::launch_mean_pool(c->blk_att, n, s.dim, 1.0f / (float)n, accum, c->stream);
+        t.done();
+        if ((rc = run(c, e, "mean pool kernel launch"))) return rc;
+    }
+    {
+        Timed t(c, SLM_K_NORM);
+        e = slm::launch_rmsnorm(accum, s.dim, nullptr, 1, s.dim, rms_eps, out, s.dim,
+                                slm::Q8Out{}, c->stream);
+        t.done();
+        if ((rc = run(c, e, "l2 norm kernel launch"))) return rc;
+    }
+    int32_t bad = 0;
+    SLM_HIP(c, hipMemcpyAsync(&bad, c->mdl_flags + 1, sizeof bad, hipMemcpyDeviceToHost,
+                              c->stream));
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
+    if (bad) return fail(c, SLM_ERR_TOKEN, "token_id out of vocabulary bounds");
+    return SLM_OK;
+}
+
+}  // extern "C"

@@ -201,3 +201,42 @@ def test_oracle_prefill_equals_sequential_decode_bitwise():
         xs[t] = row
     np.testing.assert_array_equal(xb, xs)
     np.testing.assert_array_equal(batch.kv, seq.kv)
+
+
+def ref_model():
+    """The reference's prefill test model (transformer.rs:1269-1313): dim 64,
+    4 heads over 2 KV heads, hidden 128, msl 16, vocab 128, 2 layers sharing
+    one set of weights, output_norm of ones."""
+    dim, hidden, vocab = 64, 128, 128
+    cfg = orc.Cfg(dim, 4, 2, 16, 2, 10000.0)
+    lw = ref_weights(dim, hidden, cfg.kv_dim, (0x1001, 0x2001, 0x3001))
+    w = orc.ModelWeights(token_embd=quantize_matrix(vocab, dim, 0x0100), layers=[lw, lw],
+                         output_norm=np.ones(dim, np.float32),
+                         lm_head=quantize_matrix(vocab, dim, 0x0200), vocab_size=vocab)
+    return cfg, w
+
+
+def test_sample_argmax_first_maximum_and_nan():
+    assert orc.sample_argmax(np.float32([1, 3, 3, 2])) == 1
+    assert orc.sample_argmax(np.float32([np.nan, 5, 1])) == 0
+    assert orc.sample_argmax(np.float32([1, np.nan, 5, 5])) == 2
+    assert orc.sample_argmax(np.float32([-np.inf, -np.inf])) == 0
+
+
+def test_oracle_model_prefill_first_token_matches_sequential_forward():
+    # transformer.rs:1314-1357: generate's first token (batched prefill)
+    # equals the last forward_token of a token-by-token run
+    cfg, w = ref_model()
+    prompt = [1, 7, 19, 42]
+    seq = orc.OracleModel(cfg)
+    for pos, tok in enumerate(prompt):
+        _, seq_next, _ = orc.model_forward(seq, w, 1e-5, [tok], pos)
+    out = orc.model_generate(orc.OracleModel(cfg), w, 1e-5, prompt, 4)
+    assert len(out) == 4 and out[0] == seq_next
+    assert all(0 <= t < 128 for t in out)
+
+
+def test_oracle_model_embedding_is_unit_length():
+    cfg, w = ref_model()
+    e = orc.model_embed(orc.OracleModel(cfg), w, 1e-5, [3, 9, 27, 81, 5])
+    assert abs(np.linalg.norm(e.astype(np.float64)) - 1.0) < 1e-5
