@@ -359,6 +359,89 @@ def bench_block_xb(torch, P, steps: int) -> dict:
     return {"decode_xb_32k": decode, "prefill_xb_4k": prefill}
 
 
+HIDDEN = 14336  # Llama-3-8B feed-forward width
+
+
+def layer_weight_bytes(hidden: int = HIDDEN) -> int:
+    """Q4_0 bytes of one layer's seven projections (18 B per 32 weights)."""
+    weights = 2 * DIM * DIM + 2 * KV_DIM * DIM + 3 * hidden * DIM
+    return weights // 32 * 18
+
+
+def make_layers(torch, P, rng, n: int, hidden: int = HIDDEN):
+    """n layers of random Q4_0 weights, each uploaded to its own memory (one
+    host copy per shape: timing does not depend on the values)."""
+    shapes = {"wq": (DIM, DIM), "wk": (KV_DIM, DIM), "wv": (KV_DIM, DIM), "wo": (DIM, DIM),
+              "w_gate": (hidden, DIM), "w_up": (hidden, DIM), "w_down": (DIM, hidden)}
+    host = {name: random_q4_blocks(rng, r, c) for name, (r, c) in shapes.items()}
+    norm = torch.ones(DIM, device="cuda")
+    layers = []
+    for _ in range(n):
+        m = {name: P.Q4Matrix(host[name], r, c) for name, (r, c) in shapes.items()}
+        layers.append(P.LayerWeights(norm.data_ptr(), m["wq"], m["wk"], m["wv"], m["wo"],
+                                     norm.data_ptr(), m["w_gate"], m["w_up"], m["w_down"]))
+    return layers, norm
+
+
+def bench_layer(torch, P, steps: int) -> dict:
+    """The whole transformer block (slm_layer_forward_dev), Llama-3-8B shape
+    with Q4_0 weights: one decode token through 8 distinct layers at position
+    32767 and at 4095 (weights + KV streamed from HBM), and a 4096-row
+    prefill through one layer."""
+    layers, ctx_len = 8, 32768
+    rng = np.random.default_rng(23)
+    stream = torch.cuda.current_stream()
+    ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, ctx_len, layers, THETA)
+    ctx.set_stream(stream.cuda_stream)
+    fill_cache(torch, ctx, layers, ctx_len, ctx_len, 77)
+    lws, norm = make_layers(torch, P, rng, layers)
+    x = torch.randn(DIM, device="cuda") * 0.5
+    wb = layer_weight_bytes()
+    out = {"workload": "transformer block, Llama-3-8B shape (dim 4096, 32/8 heads, hidden "
+                       "14336), Q4_0 weights, 8 distinct layers", "weight_bytes_per_layer": wb}
+    for pos in (ctx_len - 1, 4095):
+        def step():
+            for l in range(layers):
+                ctx.layer_forward_dev(l, pos, 1, lws[l], 1e-5, x.data_ptr())
+
+        ms = _ms_per_call(torch, stream, step, steps)
+        prof = _profiled(ctx, step, max(2, steps // 2))
+        per = {k: v[1] / max(v[0], 1) * 1e3 for k, v in prof.items() if v[0]}
+        nbytes = wb + 2 * (pos + 1) * KV_DIM * 4
+        us = ms / layers * 1e3
+        out[f"decode_pos{pos}"] = {
+            "us_per_layer": us, "bytes_per_layer": nbytes,
+            "gbs": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "kernel_us_mean": per,
+        }
+        log(f"layer decode @{pos}: {us:.1f} us/layer, {nbytes / (us * 1e-6) / 1e9:.0f} GB/s")
+    ctx.close()
+
+    n, msl = 4096, 4096
+    ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, msl, 1, THETA)
+    ctx.set_stream(stream.cuda_stream)
+    xs = torch.randn(n, DIM, device="cuda") * 0.5
+
+    def run():
+        ctx.layer_forward_dev(0, 0, n, lws[0], 1e-5, xs.data_ptr())
+
+    ms = _ms_per_call(torch, stream, run, 3)
+    prof = _profiled(ctx, run, 2)
+    per = {k: v[1] / max(v[0], 1) for k, v in prof.items() if v[0]}
+    weights = 2 * DIM * DIM + 2 * KV_DIM * DIM + 3 * HIDDEN * DIM
+    out["prefill_4096"] = {
+        "ms": ms, "tokens_per_s": n / (ms / 1e3),
+        "int8_tops_projections": 2 * n * weights / (prof["gemm"][1] / 1e3) / 1e12,
+        "kernel_ms_mean": per,
+    }
+    log(f"layer prefill 4096: {ms:.2f} ms, {n / (ms / 1e3):.0f} tokens/s")
+    ctx.close()
+    for lw in lws:
+        lw.close()
+    del norm
+    return out
+
+
 def bench_decode_131k(torch, P) -> dict:
     pre, steps = 131072, 64
     msl = pre + steps
@@ -515,6 +598,9 @@ def main() -> int:
     ap.add_argument("--xb-only", action="store_true",
                     help="only the attention block from xb (Q/K/V projections, attention, Wo + residual); "
                          "prints its own JSON line, not the headline one")
+    ap.add_argument("--layer-only", action="store_true",
+                    help="only the whole transformer block (decode and prefill); prints its "
+                         "own JSON line, not the headline one")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB: a plain "
                          "copy kernel of known size that scales rocprofv3 byte counters")
@@ -549,6 +635,11 @@ def main() -> int:
         log(f"copy calibration: {args.copy_calibration_mib} MiB read + "
             f"{args.copy_calibration_mib} MiB written")
         del src, dst
+
+    if args.layer_only:
+        bl = bench_layer(torch, P, max(3, args.steps // 5))
+        print(json.dumps(bl))
+        return 0
 
     if args.xb_only:
         bx = bench_block_xb(torch, P, max(3, args.steps // 5))

@@ -20,6 +20,7 @@
 #include <stdint.h>
 
 #include "attn_common.h"
+#include "jit_math.h"
 #include "quant_common.h"
 #include "slm_internal.h"
 
@@ -27,64 +28,6 @@ namespace slm {
 namespace {
 
 constexpr int kNormThreads = 256;
-
-// emit_exp_f32x4 (lower.rs:22-65), one lane: clamp to [-87.3, 88.3],
-// n = nearest(x * log2 e) (ties to even), Cody-Waite reduction with the two
-// ln 2 constants, degree-5 Horner polynomial, times 2^n built from the
-// exponent bits.  (fmaxf/fminf return the non-NaN operand where Cranelift's
-// fmax/fmin propagate NaN; the paths here never feed them NaN from finite
-// inputs.)
-__device__ __forceinline__ float jit_exp(float x) {
-#pragma clang fp contract(off)
-    float xc = fmaxf(x, -87.3f);
-    xc = fminf(xc, 88.3f);
-    const float fx = xc * 1.44269504088896340736f;
-    const float n = rintf(fx);
-    const float n_hi = n * 0.69314575f;
-    const float n_lo = n * 1.4286068e-6f;
-    const float r_hi = xc - n_hi;
-    const float r = r_hi - n_lo;
-    float p = r * (1.0f / 120.0f);
-    p = p + (1.0f / 24.0f);
-    p = r * p;
-    p = p + (1.0f / 6.0f);
-    p = r * p;
-    p = p + 0.5f;
-    p = r * p;
-    p = p + 1.0f;
-    p = r * p;
-    const float poly = p + 1.0f;
-    const int ni = (int)n;  // |n| <= 128 after the clamp
-    return poly * __int_as_float((ni + 127) << 23);
-}
-
-// Correctly rounded f32 square root (what Cranelift's `sqrt` is, x86
-// sqrtps).  v_sqrt_f32 is within 1 ulp; the exact residuals x - s'*s of its
-// neighbours s' = s -/+ 1 ulp (one fused multiply-add each, exact) tell
-// whether the rounded root is s or a neighbour.  Tiny inputs are scaled by
-// 2^32 first (root scaled by 2^16) so the residuals stay representable.
-__device__ __forceinline__ float sqrt_rn(float x) {
-    const bool tiny = x < 0x1.0p-96f;
-    const float xs = tiny ? x * 0x1.0p+32f : x;
-    float s = __builtin_amdgcn_sqrtf(xs);
-    const float s_dn = __int_as_float(__float_as_int(s) - 1);
-    const float s_up = __int_as_float(__float_as_int(s) + 1);
-    const float r_dn = __builtin_fmaf(-s_dn, s, xs);
-    const float r_up = __builtin_fmaf(-s_up, s, xs);
-    s = r_dn <= 0.0f ? s_dn : s;
-    s = r_up > 0.0f ? s_up : s;
-    s = tiny ? s * 0x1.0p-16f : s;
-    // zero, infinity and NaN pass through unchanged
-    return (xs == 0.0f || xs == __builtin_inff() || xs != xs) ? __builtin_amdgcn_sqrtf(xs) : s;
-}
-
-// SiLU lowering (lower.rs:85-91): v / (1 + exp(-v)).
-__device__ __forceinline__ float jit_silu(float v) {
-#pragma clang fp contract(off)
-    const float e = jit_exp(-v);
-    const float den = 1.0f + e;
-    return __fdiv_rn(v, den);
-}
 
 // ---- RMSNorm / L2 norm: one workgroup per row ----
 //
@@ -106,48 +49,58 @@ struct NormArgs {
 
 __host__ __device__ constexpr int norm_sq_stride(int n) { return n / 4 + 4; }
 
+// The four lane chains of the squares in s_sq (lanes 0..3 of wave 0), then
+// lane 0 combines them with the tail and returns the scale in s_scale.
+// 32 terms are added while the next 32 are read from LDS.
 template <bool RMS>
-__global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(NormArgs a) {
+__device__ __forceinline__ void norm_scale(const float* s_sq, int st, int vq, int n,
+                                           const float* s_tail, float eps, float* s_part,
+                                           float* s_scale) {
 #pragma clang fp contract(off)
-    extern __shared__ __align__(16) float s_sq[];  // [4][norm_sq_stride(n)]
-    __shared__ float s_part[4];
-    __shared__ float s_tail[4];
-    __shared__ float s_scale;
-    const int n = a.n;
-    const int vq = n / 4;  // full groups of four
-    const int st = norm_sq_stride(n);
-    const float* x = a.x + (long)blockIdx.x * a.x_stride;
     const int tid = threadIdx.x;
-
-    // squares (x2 = mul(x, x)), transposed
-    for (int i = tid; i < vq; i += kNormThreads) {
-        const float4 v = ld4(x + 4 * i);
-        s_sq[0 * st + i] = v.x * v.x;
-        s_sq[1 * st + i] = v.y * v.y;
-        s_sq[2 * st + i] = v.z * v.z;
-        s_sq[3 * st + i] = v.w * v.w;
-    }
-    if (tid < n - 4 * vq) {
-        const float v = x[4 * vq + tid];
-        s_tail[tid] = v * v;
-    }
-    __syncthreads();
-
-    if (tid < 4) {  // the four lane accumulators, in order
+    if (tid < 4) {
+        // two buffers of 32 terms take turns (no register copies between
+        // the dependent adds): one is added while the other is read
         const float* t = s_sq + tid * st;
         float acc = 0.0f;
         int i = 0;
-        for (; i + 16 <= vq; i += 16) {
-            float4 c[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) c[k] = *reinterpret_cast<const float4*>(t + i + 4 * k);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                acc = acc + c[k].x;
-                acc = acc + c[k].y;
-                acc = acc + c[k].z;
-                acc = acc + c[k].w;
+        if (vq >= 64) {
+            float4 A[8], B[8];
+#define SLM_LOAD32(buf, off)                                                              \
+    _Pragma("unroll") for (int k = 0; k < 8; ++k) buf[k] =                                \
+        *reinterpret_cast<const float4*>(t + (off) + 4 * k)
+#define SLM_ADD32(buf)                                                                    \
+    _Pragma("unroll") for (int k = 0; k < 8; ++k) {                                       \
+        acc = acc + buf[k].x;                                                             \
+        acc = acc + buf[k].y;                                                             \
+        acc = acc + buf[k].z;                                                             \
+        acc = acc + buf[k].w;                                                             \
+    }
+            SLM_LOAD32(A, 0);
+            for (; i + 96 <= vq; i += 64) {  // A holds terms [i, i + 32)
+                // the scheduling barriers keep each read group where it is:
+                // hoisting a read above the adds of the buffer it refills
+                // would make the compiler copy registers between the adds
+                SLM_LOAD32(B, i + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                SLM_ADD32(A);
+                __builtin_amdgcn_sched_barrier(0);
+                SLM_LOAD32(A, i + 64);
+                __builtin_amdgcn_sched_barrier(0);
+                SLM_ADD32(B);
+                __builtin_amdgcn_sched_barrier(0);
             }
+            if (i + 64 <= vq) {
+                SLM_LOAD32(B, i + 32);
+                SLM_ADD32(A);
+                SLM_ADD32(B);
+                i += 64;
+            } else {
+                SLM_ADD32(A);
+                i += 32;
+            }
+#undef SLM_LOAD32
+#undef SLM_ADD32
         }
         for (; i < vq; ++i) acc = acc + t[i];
         s_part[tid] = acc;
@@ -162,57 +115,139 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(NormArgs a) {
         if (RMS) {  // graph.rs:141-156
             const float inv_n = __fdiv_rn(1.0f, (float)n);
             const float mean = s * inv_n;
-            const float var = mean + a.eps;
+            const float var = mean + eps;
             scale = __fdiv_rn(1.0f, sqrt_rn(var));
         } else {    // graph.rs:182-193
-            const float var = s + a.eps;
+            const float var = s + eps;
             scale = __fdiv_rn(1.0f, sqrt_rn(var));
         }
-        s_scale = scale;
+        *s_scale = scale;
     }
+}
+
+// Rows of n % 32 == 0: quad q of the workgroup owns blocks q, q + 64, ...
+// (lane part p: elements 8p..8p+7 of each) in both phases, so x and w are
+// loaded once, up front, and held in registers across the chain.
+constexpr int kNormMaxPasses = 8;  // n <= 64 blocks * 8 passes * 32 = 16384
+
+template <bool RMS>
+__global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(NormArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) float s_sq[];  // [4][norm_sq_stride(n)]
+    __shared__ float s_part[4];
+    __shared__ float s_tail[4];
+    __shared__ float s_scale;
+    const int n = a.n;
+    const int vq = n / 4;
+    const int st = norm_sq_stride(n);
+    const float* x = a.x + (long)blockIdx.x * a.x_stride;
+    const int tid = threadIdx.x;
+    const int part = tid & 3;
+    const int nb = n / 32;
+    const int passes = (nb + 63) / 64;
+
+    float4 xr[kNormMaxPasses][2], wr[kNormMaxPasses][2];
+#pragma unroll
+    for (int k = 0; k < kNormMaxPasses; ++k) {
+        if (k >= passes) break;  // uniform
+        const int blk = min((tid >> 2) + 64 * k, nb - 1);  // clamped; not stored past nb
+        const int e0 = 32 * blk + 8 * part;
+        xr[k][0] = ld4(x + e0);
+        xr[k][1] = ld4(x + e0 + 4);
+        if (RMS) {
+            wr[k][0] = ld4(a.w + e0);
+            wr[k][1] = ld4(a.w + e0 + 4);
+        }
+    }
+    // squares, transposed: element e = 32 blk + 8 part + j goes to chain
+    // j % 4 at position 8 blk + 2 part + j / 4
+#pragma unroll
+    for (int k = 0; k < kNormMaxPasses; ++k) {
+        if (k >= passes) break;
+        const int blk = (tid >> 2) + 64 * k;
+        if (blk < nb) {
+            const int i0 = 8 * blk + 2 * part;
+            const float v[8] = {xr[k][0].x, xr[k][0].y, xr[k][0].z, xr[k][0].w,
+                                xr[k][1].x, xr[k][1].y, xr[k][1].z, xr[k][1].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s_sq[(j & 3) * st + i0 + (j >> 2)] = v[j] * v[j];
+        }
+    }
+    __syncthreads();
+    norm_scale<RMS>(s_sq, st, vq, n, s_tail, a.eps, s_part, &s_scale);
     __syncthreads();
     const float scale = s_scale;
 
-    if (a.q8.q) {
-        // quad per Q8_0 block (n % 32 == 0): 8 elements per lane
-        const int nb = n / 32;
-        const int part = tid & 3;
-        for (int blk = tid >> 2; blk < nb; blk += kNormThreads / 4) {
-            const int e0 = 32 * blk + 8 * part;
-            const float4 x0 = ld4(x + e0), x1 = ld4(x + e0 + 4);
-            float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            if (RMS) {
-                const float4 w0 = ld4(a.w + e0), w1 = ld4(a.w + e0 + 4);
-                const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float nx = v[k] * scale;
-                    v[k] = nx * wv[k];
-                }
-            } else {
+    for (int k = 0; k < kNormMaxPasses; ++k) {
+        if (k >= passes) break;
+        const int blk = (tid >> 2) + 64 * k;
+        if (blk >= nb) break;  // uniform over the quad
+        float v[8] = {xr[k][0].x, xr[k][0].y, xr[k][0].z, xr[k][0].w,
+                      xr[k][1].x, xr[k][1].y, xr[k][1].z, xr[k][1].w};
+        if (RMS) {
+            const float wv[8] = {wr[k][0].x, wr[k][0].y, wr[k][0].z, wr[k][0].w,
+                                 wr[k][1].x, wr[k][1].y, wr[k][1].z, wr[k][1].w};
 #pragma unroll
-                for (int k = 0; k < 8; ++k) v[k] = v[k] * scale;
+            for (int j = 0; j < 8; ++j) {
+                const float nx = v[j] * scale;
+                v[j] = nx * wv[j];
             }
-            if (a.out) {
-                float* o = a.out + (long)blockIdx.x * a.out_stride + e0;
-                *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
-                *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
-            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = v[j] * scale;
+        }
+        const int e0 = 32 * blk + 8 * part;
+        if (a.out) {
+            float* o = a.out + (long)blockIdx.x * a.out_stride + e0;
+            *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        if (a.q8.q)
             store_q8_quad(a.q8, blockIdx.x, blk, part, make_float4(v[0], v[1], v[2], v[3]),
                           make_float4(v[4], v[5], v[6], v[7]));
+    }
+}
+
+// Any n (f32 output only): float4 squares strided over the workgroup, the
+// tail by the first threads, elementwise output.
+template <bool RMS>
+__global__ __launch_bounds__(kNormThreads) void norm_rows_any_kernel(NormArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) float s_sq[];
+    __shared__ float s_part[4];
+    __shared__ float s_tail[4];
+    __shared__ float s_scale;
+    const int n = a.n;
+    const int vq = n / 4;
+    const int st = norm_sq_stride(n);
+    const float* x = a.x + (long)blockIdx.x * a.x_stride;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < vq; i += kNormThreads) {
+        const float4 v = ld4(x + 4 * i);
+        s_sq[0 * st + i] = v.x * v.x;
+        s_sq[1 * st + i] = v.y * v.y;
+        s_sq[2 * st + i] = v.z * v.z;
+        s_sq[3 * st + i] = v.w * v.w;
+    }
+    if (tid < n - 4 * vq) {
+        const float v = x[4 * vq + tid];
+        s_tail[tid] = v * v;
+    }
+    __syncthreads();
+    norm_scale<RMS>(s_sq, st, vq, n, s_tail, a.eps, s_part, &s_scale);
+    __syncthreads();
+    const float scale = s_scale;
+    float* o = a.out + (long)blockIdx.x * a.out_stride;
+    for (int e = tid; e < n; e += kNormThreads) {
+        float y;
+        if (RMS) {
+            const float nx = x[e] * scale;
+            y = nx * a.w[e];
+        } else {
+            y = x[e] * scale;
         }
-    } else {
-        float* o = a.out + (long)blockIdx.x * a.out_stride;
-        for (int e = tid; e < n; e += kNormThreads) {
-            float y;
-            if (RMS) {
-                const float nx = x[e] * scale;
-                y = nx * a.w[e];
-            } else {
-                y = x[e] * scale;
-            }
-            o[e] = y;
-        }
+        o[e] = y;
     }
 }
 
@@ -363,13 +398,18 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, 
 template <bool RMS>
 hipError_t launch_norm_t(const NormArgs& a, int rows, hipStream_t st) {
     const size_t lds = (size_t)4 * norm_sq_stride(a.n) * sizeof(float);
+    const bool blocks = a.n % 32 == 0;
+    const void* fn = blocks ? reinterpret_cast<const void*>(norm_rows_kernel<RMS>)
+                            : reinterpret_cast<const void*>(norm_rows_any_kernel<RMS>);
     if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(norm_rows_kernel<RMS>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const hipError_t e =
+            hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(norm_rows_kernel<RMS>, dim3(rows), dim3(kNormThreads), lds, st, a);
+    if (blocks)
+        hipLaunchKernelGGL(norm_rows_kernel<RMS>, dim3(rows), dim3(kNormThreads), lds, st, a);
+    else
+        hipLaunchKernelGGL(norm_rows_any_kernel<RMS>, dim3(rows), dim3(kNormThreads), lds, st, a);
     return hipGetLastError();
 }
 

@@ -26,6 +26,7 @@
 #include <stdint.h>
 
 #include "attn_common.h"
+#include "jit_math.h"
 #include "quant_common.h"
 #include "slm_internal.h"
 
@@ -392,6 +393,105 @@ __global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
     }
 }
 
+// ---- gate and up from pre-quantized activations, SwiGLU fused ----
+//
+// FuseGraph::swiglu (graph.rs:131-139) reads the gate and up rows of the same
+// hidden index, so a workgroup takes 32 hidden rows of both matrices (wave w:
+// rows 8w..8w+7 of each, 16 row streams) and, once its ordered sums are done,
+// one quad forms act = silu(gate) * up for the 32 rows and quantizes them as
+// the one Q8_0 block the down projection reads (quantize_row_q8_0 of act).
+// Gate, up and act carry the same bits as the separate kernels give.
+
+constexpr int kSwRowsPerWave = 8;             // hidden rows per wave (of each matrix)
+constexpr int kSwRows = 4 * kSwRowsPerWave;   // hidden rows per workgroup: one Q8_0 block
+
+struct GemvSwigluParams {
+    QMat gate, up;       // [hidden][nb]; out/res unused
+    const uint32_t* aq;  // [nb][8]
+    const float* ad;     // [nb]
+    const int* as;       // [nb]
+    int nb;
+    float* act;          // [hidden] f32, or nullptr
+    Q8Out q8;            // act as Q8_0 blocks (one row of hidden / 32 blocks)
+};
+
+template <int NBL>
+__global__ __launch_bounds__(256) void gemv_q8in_swiglu_kernel(GemvSwigluParams p) {
+#pragma clang fp contract(off)
+    constexpr int R = 2 * kSwRowsPerWave;  // row streams per wave: gate rows, then up rows
+    __shared__ __align__(16) float s_t[4][R][kTermStride];
+    __shared__ float s_g[kSwRows], s_u[kSwRows];
+    const int nb = p.nb;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int h0 = blockIdx.x * kSwRows;             // the workgroup's block of hidden rows
+    const int hw = h0 + wave * kSwRowsPerWave;       // this wave's first row
+
+    uint4 a0[NBL], a1[NBL];
+    float da[NBL];
+    int as[NBL];
+    uint4 wq[NBL][R];
+    uint16_t wd[NBL][R];
+#define SLM_SW_ISSUE(j)                                                                      \
+    do {                                                                                     \
+        const int b_ = min(kChunk * (j) + lane, nb - 1);                                     \
+        a0[j] = *reinterpret_cast<const uint4*>(p.aq + (long)b_ * 8);                        \
+        a1[j] = *reinterpret_cast<const uint4*>(p.aq + (long)b_ * 8 + 4);                    \
+        da[j] = p.ad[b_];                                                                    \
+        as[j] = p.as[b_];                                                                    \
+        _Pragma("unroll") for (int rr = 0; rr < R; ++rr) {                                   \
+            const QMat& M_ = rr < kSwRowsPerWave ? p.gate : p.up;                            \
+            const long r_ = hw + (rr % kSwRowsPerWave);                                      \
+            wq[j][rr] = *reinterpret_cast<const uint4*>(M_.qs + (r_ * nb + b_) * 16);        \
+            wd[j][rr] = M_.d[r_ * M_.d_stride + b_];                                         \
+        }                                                                                    \
+    } while (0)
+#pragma unroll
+    for (int j = 0; j < (kPrefetch < NBL ? kPrefetch : NBL); ++j) SLM_SW_ISSUE(j);
+
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NBL; ++j) {  // NBL = ceil(nb / kChunk)
+        if (j + kPrefetch < NBL) SLM_SW_ISSUE(j + kPrefetch);
+        __builtin_amdgcn_sched_barrier(0);
+        const int b0 = kChunk * j;
+        if (b0 + lane < nb) {
+            const uint32_t a[8] = {a0[j].x, a0[j].y, a0[j].z, a0[j].w,
+                                   a1[j].x, a1[j].y, a1[j].z, a1[j].w};
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) {
+                const int isum = block_dot(wq[j][rr], a, as[j]);
+                s_t[wave][rr][lane] = (float)isum * (h2f(wd[j][rr]) * da[j]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < R) acc = ordered_add(acc, &s_t[wave][lane][0], min(kChunk, nb - b0));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+#undef SLM_SW_ISSUE
+
+    if (lane < kSwRowsPerWave) s_g[wave * kSwRowsPerWave + lane] = acc;
+    else if (lane < R) s_u[wave * kSwRowsPerWave + lane - kSwRowsPerWave] = acc;
+    __syncthreads();
+    if (threadIdx.x < 4) {  // one quad: elements 8p..8p+7 of the block
+        const int part = threadIdx.x;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = jit_silu(s_g[8 * part + k]) * s_u[8 * part + k];
+        const float4 f0 = make_float4(v[0], v[1], v[2], v[3]);
+        const float4 f1 = make_float4(v[4], v[5], v[6], v[7]);
+        if (p.act) {
+            *reinterpret_cast<float4*>(p.act + h0 + 8 * part) = f0;
+            *reinterpret_cast<float4*>(p.act + h0 + 8 * part + 4) = f1;
+        }
+        store_q8_quad(p.q8, 0, blockIdx.x, part, f0, f1);
+    }
+}
+
 // ---- MFMA GEMM: batches of 5 or more tokens ----
 //
 // Workgroup tile 64 rows x 64 tokens, four waves of 32 x 32 (2 x 2 tiles of
@@ -700,6 +800,33 @@ hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, c
         SLM_GEMV_Q8_CASE(1) SLM_GEMV_Q8_CASE(2) SLM_GEMV_Q8_CASE(3) SLM_GEMV_Q8_CASE(4)
         SLM_GEMV_Q8_CASE(5) SLM_GEMV_Q8_CASE(6) SLM_GEMV_Q8_CASE(7) SLM_GEMV_Q8_CASE(8)
 #undef SLM_GEMV_Q8_CASE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_q4_gemv_q8_swiglu(const Q4Job& gate, const Q4Job& up, const uint32_t* aq,
+                                    const float* ad, const int* as, int nb, float* act,
+                                    const Q8Out& q8, hipStream_t st) {
+    const int hidden = gate.rows;
+    if (up.rows != hidden || hidden % kSwRows || nb < 1 || nb > 8 * kChunk || !q8.q)
+        return hipErrorInvalidValue;
+    GemvSwigluParams p{};
+    p.gate = QMat{gate.qs, gate.d, nullptr, nullptr, hidden, 0, q4_scale_stride(nb)};
+    p.up = QMat{up.qs, up.d, nullptr, nullptr, hidden, 0, q4_scale_stride(nb)};
+    p.aq = aq;
+    p.ad = ad;
+    p.as = as;
+    p.nb = nb;
+    p.act = act;
+    p.q8 = q8;
+    const int grid = hidden / kSwRows;
+    switch ((nb + kChunk - 1) / kChunk) {
+#define SLM_SW_CASE(n) \
+    case n: hipLaunchKernelGGL(gemv_q8in_swiglu_kernel<n>, dim3(grid), dim3(256), 0, st, p); break;
+        SLM_SW_CASE(1) SLM_SW_CASE(2) SLM_SW_CASE(3) SLM_SW_CASE(4)
+        SLM_SW_CASE(5) SLM_SW_CASE(6) SLM_SW_CASE(7) SLM_SW_CASE(8)
+#undef SLM_SW_CASE
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

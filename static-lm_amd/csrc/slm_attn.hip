@@ -263,6 +263,19 @@ int ensure_q8(slm_attn_ctx* c, size_t n, int nb) {
     return SLM_OK;
 }
 
+int ensure_q8x(slm_attn_ctx* c, size_t n, int nb) {
+    const size_t blocks = n * (size_t)slm::q4_scale_stride(nb);
+    size_t have_q = c->q8x_blocks * 8, have_d = c->q8x_blocks, have_s = c->q8x_blocks;
+    int rc = ensure_buffer(c, &c->q8x_q, &have_q, blocks * 8, "hipMalloc(q8 activations)");
+    if (rc) return rc;
+    rc = ensure_buffer(c, &c->q8x_d, &have_d, blocks, "hipMalloc(q8 scales)");
+    if (rc) return rc;
+    rc = ensure_buffer(c, &c->q8x_s, &have_s, blocks, "hipMalloc(q8 sums)");
+    if (rc) return rc;
+    if (blocks > c->q8x_blocks) c->q8x_blocks = blocks;
+    return SLM_OK;
+}
+
 int check_matrix(slm_attn_ctx* c, const slm_q4_matrix* m, int rows, int cols, const char* name) {
     if (!m) return fail(c, SLM_ERR_ARG, std::string(name) + " is NULL");
     if (m->device != c->device)
@@ -497,6 +510,9 @@ void slm_attn_destroy(slm_attn_ctx* c) {
     (void)hipFree(c->q8_q);
     (void)hipFree(c->q8_d);
     (void)hipFree(c->q8_s);
+    (void)hipFree(c->q8x_q);
+    (void)hipFree(c->q8x_d);
+    (void)hipFree(c->q8x_s);
     (void)hipFree(c->qkv);
     (void)hipFree(c->blk_att);
     (void)hipFree(c->blk_mid);

@@ -51,6 +51,12 @@ struct slm_attn_ctx {
     float* q8_d = nullptr;
     int* q8_s = nullptr;  // blocks' sums of quantized values (the GEMV's input)
     size_t q8_blocks = 0;
+    // a second set, for a kernel that reads one Q8_0 activation and writes
+    // another (the fused gate/up + SwiGLU projection)
+    uint32_t* q8x_q = nullptr;
+    float* q8x_d = nullptr;
+    int* q8x_s = nullptr;
+    size_t q8x_blocks = 0;
     float* qkv = nullptr;
     size_t qkv_floats = 0;
     // transformer block workspace (slm_layer.h): attention rows and x_mid
@@ -157,6 +163,7 @@ int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* 
 int do_attend(slm_attn_ctx* c, int layer, int start, int n, const float* q, float* out,
               bool rotate);
 int ensure_q8(slm_attn_ctx* c, size_t n, int nb);
+int ensure_q8x(slm_attn_ctx* c, size_t n, int nb);
 int check_matrix(slm_attn_ctx* c, const slm_q4_matrix* m, int rows, int cols, const char* name);
 slm::Q4Job q4_job(const slm_q4_matrix* m, float* out, const float* res = nullptr);
 int project(slm_attn_ctx* c, const slm_q4_matrix* w, const float* x, int batch, float* out,

@@ -117,6 +117,12 @@ struct Q8Out {
     int nb;
     int d_stride;
 };
+// gate and up rows of one token from pre-quantized activations with SwiGLU
+// fused: act = silu(gate . x) * (up . x) for every hidden row, written as
+// Q8_0 blocks to q8 (and f32 to act unless nullptr); hidden % 32 == 0
+hipError_t launch_q4_gemv_q8_swiglu(const Q4Job& gate, const Q4Job& up, const uint32_t* aq,
+                                    const float* ad, const int* as, int nb, float* act,
+                                    const Q8Out& q8, hipStream_t st);
 // any batch, from pre-quantized activations
 hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
                           int nb, int batch, hipStream_t st);

@@ -128,6 +128,7 @@ int slm_layer_forward_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t
     const int nb = s.dim / 32, nbh = hidden / 32;
     const size_t per_row = (size_t)s.dim + 2 * (size_t)s.kv_dim;
     if ((rc = ensure_q8(c, (size_t)n, nbh > nb ? nbh : nb)) ||
+        (n == 1 && (rc = ensure_q8x(c, 1, nbh))) ||
         (rc = ensure_buffer(c, &c->qkv, &c->qkv_floats, (size_t)n * per_row,
                             "hipMalloc(qkv rows)")) ||
         (rc = ensure_buffer(c, &c->blk_att, &c->blk_att_floats, nd, "hipMalloc(block rows)")) ||
@@ -180,16 +181,34 @@ int slm_layer_forward_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t
         t.done();
         if ((rc = run(c, e, "rmsnorm kernel launch"))) return rc;
     }
-    // gate and up (:456-473 / 617-636)
+    if (one) {
+        // gate and up with SwiGLU fused, act straight to Q8_0 blocks in the
+        // second activation buffer (:456-475)
+        {
+            const slm::Q4Job gate = q4_job(w->w_gate, nullptr), up = q4_job(w->w_up, nullptr);
+            const slm::Q8Out act{c->q8x_q, c->q8x_d, c->q8x_s, nbh, slm::q4_scale_stride(nbh)};
+            Timed t(c, SLM_K_GEMM);
+            hipError_t e = slm::launch_q4_gemv_q8_swiglu(gate, up, c->q8_q, c->q8_d, c->q8_s, nb,
+                                                         nullptr, act, st);
+            t.done();
+            if ((rc = run(c, e, "q4 projection kernel launch"))) return rc;
+        }
+        // x = x_mid + W_down . act (:477-486)
+        const slm::Q4Job job = q4_job(w->w_down, x, x_mid);
+        Timed t(c, SLM_K_GEMM);
+        hipError_t e = slm::launch_q4_gemv_q8(&job, 1, c->q8x_q, c->q8x_d, c->q8x_s, nbh, st);
+        t.done();
+        return run(c, e, "q4 projection kernel launch");
+    }
+    // gate and up (:617-636)
     {
         const slm::Q4Job jobs[2] = {q4_job(w->w_gate, hb), q4_job(w->w_up, hb2)};
         Timed t(c, SLM_K_GEMM);
-        hipError_t e = one ? slm::launch_q4_gemv_q8(jobs, 2, c->q8_q, c->q8_d, c->q8_s, nb, st)
-                           : slm::launch_q4_gemm(jobs, 2, c->q8_q, c->q8_d, nb, n, st);
+        hipError_t e = slm::launch_q4_gemm(jobs, 2, c->q8_q, c->q8_d, nb, n, st);
         t.done();
         if ((rc = run(c, e, "q4 projection kernel launch"))) return rc;
     }
-    // SwiGLU straight to Q8_0 (:475 / 638)
+    // SwiGLU straight to Q8_0 (:638)
     {
         Timed t(c, SLM_K_ELEM);
         hipError_t e = slm::launch_swiglu(hb, hb2, (long)n * hidden, hidden, nullptr,
@@ -197,16 +216,12 @@ int slm_layer_forward_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t
         t.done();
         if ((rc = run(c, e, "swiglu kernel launch"))) return rc;
     }
-    // x = x_mid + W_down . act (:477-486 / 640-650)
-    {
-        const slm::Q4Job job = q4_job(w->w_down, x, x_mid);
-        Timed t(c, SLM_K_GEMM);
-        hipError_t e = one ? slm::launch_q4_gemv_q8(&job, 1, c->q8_q, c->q8_d, c->q8_s, nbh, st)
-                           : slm::launch_q4_gemm(&job, 1, c->q8_q, c->q8_d, nbh, n, st);
-        t.done();
-        if ((rc = run(c, e, "q4 projection kernel launch"))) return rc;
-    }
-    return SLM_OK;
+    // x = x_mid + W_down . act (:640-650)
+    const slm::Q4Job job = q4_job(w->w_down, x, x_mid);
+    Timed t(c, SLM_K_GEMM);
+    hipError_t e = slm::launch_q4_gemm(&job, 1, c->q8_q, c->q8_d, nbh, n, st);
+    t.done();
+    return run(c, e, "q4 projection kernel launch");
 }
 
 }  // extern "C"
