@@ -27,6 +27,7 @@ HEADER_PATH = PKG_DIR.parent / "include" / "slm_attn.h"
 CALIB_HEADER_PATH = PKG_DIR.parent / "include" / "slm_calib.h"
 QUANT_HEADER_PATH = PKG_DIR.parent / "include" / "slm_quant.h"
 LAYER_HEADER_PATH = PKG_DIR.parent / "include" / "slm_layer.h"
+GGUF_HEADER_PATH = PKG_DIR.parent / "include" / "slm_gguf.h"
 
 SLM_OK = 0
 ERRORS = {
@@ -41,9 +42,23 @@ ERRORS = {
     -9: "SLM_ERR_DEVICE",
     -10: "SLM_ERR_SHAPE",
     -11: "SLM_ERR_TOKEN",
+    -12: "SLM_ERR_IO",
+    -13: "SLM_ERR_EOF",
+    -14: "SLM_ERR_MAGIC",
+    -15: "SLM_ERR_VERSION",
+    -16: "SLM_ERR_UTF8",
+    -17: "SLM_ERR_VALUE_TYPE",
+    -18: "SLM_ERR_DIMS",
+    -19: "SLM_ERR_NOT_FOUND",
+    -20: "SLM_ERR_TYPE",
+    -21: "SLM_ERR_BOUNDS",
+    -22: "SLM_ERR_UNALIGNED",
 }
 (ERR_CONFIG, ERR_POS, ERR_BATCH, ERR_LAYER, ERR_ALIAS, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED,
  ERR_DEVICE, ERR_SHAPE, ERR_TOKEN) = (-1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11)
+(ERR_IO, ERR_EOF, ERR_MAGIC, ERR_VERSION, ERR_UTF8, ERR_VALUE_TYPE, ERR_DIMS, ERR_NOT_FOUND,
+ ERR_TYPE, ERR_BOUNDS, ERR_UNALIGNED) = tuple(range(-12, -23, -1))
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8
 
 KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope", "quant", "gemm", "norm",
                 "elem")
@@ -149,7 +164,49 @@ SIGNATURES = {
     "slm_model_prefill_dev": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _I, _I, _P, _P]),
     "slm_model_generate_dev": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _I, _P, _I, _I, _P]),
     "slm_model_embed_dev": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _I, _P]),
+    "slm_gguf_open": (ctypes.c_int, [ctypes.c_char_p, _P]),
+    "slm_gguf_close": (None, [_P]),
+    "slm_gguf_version": (ctypes.c_int32, [_P]),
+    "slm_gguf_alignment": (ctypes.c_int64, [_P]),
+    "slm_gguf_data_offset": (ctypes.c_int64, [_P]),
+    "slm_gguf_tensor_count": (ctypes.c_int64, [_P]),
+    "slm_gguf_kv_count": (ctypes.c_int64, [_P]),
+    "slm_gguf_get": (ctypes.c_int, [_P, ctypes.c_char_p, _P]),
+    "slm_gguf_get_u32": (ctypes.c_int, [_P, ctypes.c_char_p, _P]),
+    "slm_gguf_get_usize": (ctypes.c_int, [_P, ctypes.c_char_p, _P]),
+    "slm_gguf_get_f32": (ctypes.c_int, [_P, ctypes.c_char_p, _P]),
+    "slm_gguf_get_str": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P]),
+    "slm_gguf_tensor_info": (ctypes.c_int, [_P, ctypes.c_char_p, _P]),
+    "slm_gguf_tensor_data": (ctypes.c_int, [_P, ctypes.c_char_p, _I, _P, _P]),
+    "slm_gguf_model_config": (ctypes.c_int, [_P, _P]),
+    "slm_model_load_gguf": (ctypes.c_int, [_P, _I, _I, _P]),
+    "slm_model_destroy": (None, [_P]),
+    "slm_model_weights_view": (_P, [_P]),
+    "slm_model_vocab_size": (ctypes.c_int32, [_P]),
 }
+
+
+class GgufValueC(ctypes.Structure):
+    """slm_gguf_value (include/slm_gguf.h)."""
+    _fields_ = [("type", ctypes.c_int32), ("i64", ctypes.c_int64), ("u64", ctypes.c_uint64),
+                ("f64", ctypes.c_double), ("str", ctypes.c_void_p), ("str_len", ctypes.c_uint64),
+                ("elem_type", ctypes.c_int32), ("len", ctypes.c_uint64),
+                ("byte_offset", ctypes.c_uint64), ("byte_len", ctypes.c_uint64)]
+
+
+class GgufTensorC(ctypes.Structure):
+    """slm_gguf_tensor (include/slm_gguf.h)."""
+    _fields_ = [("ggml_type", ctypes.c_int32), ("n_dims", ctypes.c_int32),
+                ("dims", ctypes.c_uint64 * 4), ("offset", ctypes.c_uint64),
+                ("n_elements", ctypes.c_uint64)]
+
+
+class ModelConfigC(ctypes.Structure):
+    """slm_model_config (include/slm_gguf.h)."""
+    _fields_ = [("dim", ctypes.c_int32), ("hidden_dim", ctypes.c_int32),
+                ("num_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
+                ("max_seq_len", ctypes.c_int32), ("num_layers", ctypes.c_int32),
+                ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
 
 
 class LayerWeightsC(ctypes.Structure):
@@ -515,11 +572,153 @@ class ModelWeights:
                              self.output_norm, self.lm_head.handle)
 
 
+def _raise(lib, rc: int) -> None:
+    if rc != SLM_OK:
+        raise SlmAttnError(rc, lib.slm_attn_last_error(None).decode())
+
+
+class GgufFile:
+    """A GGUF v2/v3 file, memory-mapped (slm_gguf_open; GgufFile::open,
+    loader.rs:330-400)."""
+
+    def __init__(self, path):
+        self.lib = load_library()
+        h = _P()
+        _raise(self.lib, self.lib.slm_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def version(self) -> int:
+        return self.lib.slm_gguf_version(self._h)
+
+    @property
+    def alignment(self) -> int:
+        return self.lib.slm_gguf_alignment(self._h)
+
+    @property
+    def data_offset(self) -> int:
+        return self.lib.slm_gguf_data_offset(self._h)
+
+    @property
+    def tensor_count(self) -> int:
+        return self.lib.slm_gguf_tensor_count(self._h)
+
+    @property
+    def kv_count(self) -> int:
+        return self.lib.slm_gguf_kv_count(self._h)
+
+    def get(self, key: str) -> GgufValueC:
+        v = GgufValueC()
+        _raise(self.lib, self.lib.slm_gguf_get(self._h, key.encode(), ctypes.byref(v)))
+        return v
+
+    def get_u32(self, key: str) -> int:
+        v = ctypes.c_uint32()
+        _raise(self.lib, self.lib.slm_gguf_get_u32(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def get_usize(self, key: str) -> int:
+        v = ctypes.c_uint64()
+        _raise(self.lib, self.lib.slm_gguf_get_usize(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def get_f32(self, key: str) -> float:
+        v = ctypes.c_float()
+        _raise(self.lib, self.lib.slm_gguf_get_f32(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def get_str(self, key: str) -> str:
+        p, n = ctypes.c_void_p(), ctypes.c_uint64()
+        _raise(self.lib, self.lib.slm_gguf_get_str(self._h, key.encode(), ctypes.byref(p),
+                                                   ctypes.byref(n)))
+        return ctypes.string_at(p.value, n.value).decode() if n.value else ""
+
+    def tensor_info(self, name: str) -> GgufTensorC:
+        t = GgufTensorC()
+        _raise(self.lib, self.lib.slm_gguf_tensor_info(self._h, name.encode(), ctypes.byref(t)))
+        return t
+
+    def tensor_view(self, name: str, ggml_type: int) -> tuple[int, int]:
+        """(address in the mapping, byte length) of a checked tensor view."""
+        p, n = ctypes.c_void_p(), ctypes.c_uint64()
+        _raise(self.lib, self.lib.slm_gguf_tensor_data(self._h, name.encode(), ggml_type,
+                                                       ctypes.byref(p), ctypes.byref(n)))
+        return p.value or 0, n.value
+
+    def tensor_bytes(self, name: str, ggml_type: int) -> bytes:
+        addr, n = self.tensor_view(name, ggml_type)
+        return ctypes.string_at(addr, n) if n else b""
+
+    def model_config(self) -> dict:
+        c = ModelConfigC()
+        _raise(self.lib, self.lib.slm_gguf_model_config(self._h, ctypes.byref(c)))
+        return {f: getattr(c, f) for f, _ in ModelConfigC._fields_}
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.slm_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class GgufModel:
+    """A whole model uploaded from a GgufFile (slm_model_load_gguf); usable
+    wherever a ModelWeights is (its c() is the library's own view)."""
+
+    def __init__(self, gguf: GgufFile, num_layers: int, device: int = 0):
+        self.lib = load_library()
+        h = _P()
+        _raise(self.lib, self.lib.slm_model_load_gguf(gguf.handle, device, num_layers,
+                                                      ctypes.byref(h)))
+        self._h = h
+
+    @property
+    def vocab_size(self) -> int:
+        return self.lib.slm_model_vocab_size(self._h)
+
+    def c(self) -> "ModelWeightsC":
+        return ctypes.cast(self.lib.slm_model_weights_view(self._h),
+                           ctypes.POINTER(ModelWeightsC)).contents
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.slm_model_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def header_functions(*headers: os.PathLike | str) -> list[str]:
     """Names of the functions the given headers (default: every include/*.h) declare."""
     import re
 
-    paths = headers or (HEADER_PATH, CALIB_HEADER_PATH, QUANT_HEADER_PATH, LAYER_HEADER_PATH)
+    paths = headers or (HEADER_PATH, CALIB_HEADER_PATH, QUANT_HEADER_PATH, LAYER_HEADER_PATH,
+                        GGUF_HEADER_PATH)
     names = set()
     for h in paths:
         names |= set(re.findall(r"\b(slm_[a-z0-9_]+)\s*\(", Path(h).read_text()))

@@ -21,8 +21,13 @@ LIB = PKG_DIR / "libslm_attn.so"
 HOST_DEMO = PKG_DIR / "slm_host_demo"
 BUILD_DIR = PKG_DIR / "_build"
 
-HIP_SOURCES = ["slm_attn.hip", "slm_layer.hip", "rope_append.hip", "attn_decode.hip", "prefill_mfma.hip",
-               "quant_gemm.hip", "norm_act.hip", "calib.hip"]
+HIP_SOURCES = ["slm_attn.hip", "slm_layer.hip", "slm_model.hip", "rope_append.hip",
+               "attn_decode.hip", "prefill_mfma.hip", "quant_gemm.hip", "norm_act.hip",
+               "calib.hip"]
+# host-only C++ (no device code), compiled with the host compiler
+CPP_SOURCES = ["gguf.cpp"]
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Werror",
+             f"-I{REPO / 'include'}", f"-I{CSRC}"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
@@ -57,6 +62,10 @@ def build_library(jobs: int = 4) -> Path:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         objs.append(obj)
         cmds.append([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    for src in CPP_SOURCES:
+        obj = BUILD_DIR / (Path(src).stem + ".o")
+        objs.append(obj)
+        cmds.append(["g++", *CXX_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     tmp = LIB.with_suffix(".so.tmp")

@@ -1,0 +1,130 @@
+// Device upload of a GGUF model (slm_gguf.h): GgufFile::model_weights
+// (loader.rs:508-552) resolved by tensor name and copied to one device as
+// slm_q4_matrix handles and f32 vectors, with the slm_model_weights view the
+// slm_model_*_dev entry points take.
+#include "../../include/slm_gguf.h"
+
+#include <string>
+#include <vector>
+
+#include "slm_host.h"
+
+using namespace slm_host;
+
+struct slm_model {
+    int device = 0;
+    int vocab = 0;
+    std::vector<slm_q4_matrix*> mats;  // owned
+    std::vector<float*> vecs;          // owned device f32 vectors
+    std::vector<slm_layer_weights> layers;
+    slm_model_weights view{};
+};
+
+namespace {
+
+// A Q4_0 tensor [dims[1..]][dims[0]] as a rows x cols matrix on the device.
+int load_q4(slm_model* m, const slm_gguf* g, const std::string& name,
+            const slm_q4_matrix** out) {
+    slm_gguf_tensor t;
+    const void* data;
+    uint64_t bytes;
+    int rc;
+    if ((rc = slm_gguf_tensor_info(g, name.c_str(), &t)) ||
+        (rc = slm_gguf_tensor_data(g, name.c_str(), SLM_GGML_Q4_0, &data, &bytes)))
+        return rc;
+    const uint64_t cols = t.dims[0], rows = cols ? t.n_elements / cols : 0;
+    if (cols == 0 || rows == 0 || rows > INT32_MAX || cols > INT32_MAX)
+        return fail(nullptr, SLM_ERR_SHAPE, name + " has an empty or oversized shape");
+    slm_q4_matrix* q = nullptr;
+    if ((rc = slm_q4_matrix_create(m->device, data, (int32_t)rows, (int32_t)cols, &q))) return rc;
+    m->mats.push_back(q);
+    *out = q;
+    return SLM_OK;
+}
+
+int load_f32(slm_model* m, const slm_gguf* g, const std::string& name, const float** out) {
+    const void* data;
+    uint64_t bytes;
+    int rc;
+    if ((rc = slm_gguf_tensor_data(g, name.c_str(), SLM_GGML_F32, &data, &bytes))) return rc;
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    float* d = nullptr;
+    hipError_t e = hipSetDevice(m->device);
+    if (e == hipSuccess) e = hipMalloc(&d, bytes ? bytes : 4);
+    if (e == hipSuccess) m->vecs.push_back(d);
+    if (e == hipSuccess && bytes) e = hipMemcpy(d, data, bytes, hipMemcpyHostToDevice);
+    if (prev >= 0) (void)hipSetDevice(prev);
+    if (e != hipSuccess) return hip_fail(nullptr, e, "f32 tensor upload");
+    *out = d;
+    return SLM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int slm_model_load_gguf(const slm_gguf* g, int32_t device, int32_t num_layers,
+                        slm_model** out) {
+    if (!out) return fail(nullptr, SLM_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    if (!g) return fail(nullptr, SLM_ERR_ARG, "gguf is NULL");
+    if (num_layers < 1) return fail(nullptr, SLM_ERR_CONFIG, "num_layers must be positive");
+    slm_model* m = new slm_model();
+    m->device = device;
+    auto bail = [&](int rc) {
+        slm_model_destroy(m);
+        return rc;
+    };
+    int rc;
+    slm_gguf_tensor embd;
+    if ((rc = slm_gguf_tensor_info(g, "token_embd.weight", &embd))) return bail(rc);
+    if (embd.dims[1] > INT32_MAX)
+        return bail(fail(nullptr, SLM_ERR_BOUNDS, "OutOfBounds(token_embd.weight)"));
+    m->vocab = (int)embd.dims[1];
+    const slm_q4_matrix* token_embd = nullptr;
+    const slm_q4_matrix* lm_head = nullptr;
+    const float* output_norm = nullptr;
+    if ((rc = load_q4(m, g, "token_embd.weight", &token_embd)) ||
+        (rc = load_f32(m, g, "output_norm.weight", &output_norm)))
+        return bail(rc);
+    slm_gguf_tensor out_info;
+    if (slm_gguf_tensor_info(g, "output.weight", &out_info) == SLM_OK) {
+        if ((rc = load_q4(m, g, "output.weight", &lm_head))) return bail(rc);
+    } else {
+        lm_head = token_embd;  // tied embeddings (loader.rs:535-539)
+    }
+    m->layers.resize((size_t)num_layers);
+    for (int l = 0; l < num_layers; ++l) {  // layer_weights (loader.rs:508-521)
+        const std::string p = "blk." + std::to_string(l) + ".";
+        slm_layer_weights& lw = m->layers[(size_t)l];
+        if ((rc = load_f32(m, g, p + "attn_norm.weight", &lw.rms_att)) ||
+            (rc = load_q4(m, g, p + "attn_q.weight", &lw.wq)) ||
+            (rc = load_q4(m, g, p + "attn_k.weight", &lw.wk)) ||
+            (rc = load_q4(m, g, p + "attn_v.weight", &lw.wv)) ||
+            (rc = load_q4(m, g, p + "attn_output.weight", &lw.wo)) ||
+            (rc = load_f32(m, g, p + "ffn_norm.weight", &lw.rms_ffn)) ||
+            (rc = load_q4(m, g, p + "ffn_gate.weight", &lw.w_gate)) ||
+            (rc = load_q4(m, g, p + "ffn_up.weight", &lw.w_up)) ||
+            (rc = load_q4(m, g, p + "ffn_down.weight", &lw.w_down)))
+            return bail(rc);
+    }
+    m->view = slm_model_weights{token_embd, m->layers.data(), num_layers, output_norm, lm_head};
+    *out = m;
+    return SLM_OK;
+}
+
+void slm_model_destroy(slm_model* m) {
+    if (!m) return;
+    for (slm_q4_matrix* q : m->mats) slm_q4_matrix_destroy(q);
+    for (float* v : m->vecs) (void)hipFree(v);
+    delete m;
+}
+
+const slm_model_weights* slm_model_weights_view(const slm_model* m) {
+    return m ? &m->view : nullptr;
+}
+
+int32_t slm_model_vocab_size(const slm_model* m) { return m ? m->vocab : 0; }
+
+}  // extern "C"

@@ -77,6 +77,6 @@ def test_create_rejects_uncompiled_head_dim():
 
 def test_header_declares_error_codes_the_binding_uses():
     text = "".join(h.read_text() for h in (P.HEADER_PATH, P.QUANT_HEADER_PATH,
-                                             P.LAYER_HEADER_PATH))
+                                             P.LAYER_HEADER_PATH, P.GGUF_HEADER_PATH))
     for code, name in P.ERRORS.items():
         assert f"#define {name} ({code})" in text
