@@ -673,6 +673,8 @@ def main() -> int:
             f"QKV GEMV {bx['decode_xb_32k']['gemv_us']:.2f} us "
             f"({bx['decode_xb_32k']['gemv_gbs']:.0f} GB/s); prefill block 4k "
             f"{bx['prefill_xb_4k']['ms']:.3f} ms (GEMM {bx['prefill_xb_4k']['gemm_ms']:.3f} ms)")
+        log("transformer block")
+        blk = bench_layer(torch, P, max(3, args.steps // 5))
         log("calibration")
         cal_mfma = P.calibrate_mfma_f32(iters=20000)
         cal_nt = P.calibrate_hbm_read(4 << 30, nontemporal=True)
@@ -700,6 +702,7 @@ def main() -> int:
             },
             "configs": wl,
             **bx,
+            "transformer_block": blk,
         }
     cpu = None
     if args.cpu_seconds > 0:
