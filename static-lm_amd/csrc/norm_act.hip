@@ -21,6 +21,7 @@
 
 #include "attn_common.h"
 #include "jit_math.h"
+#include "norm_common.h"
 #include "quant_common.h"
 #include "slm_internal.h"
 
@@ -47,84 +48,6 @@ struct NormArgs {
     Q8Out q8;         // Q8_0 output of each row, or q8.q == nullptr
 };
 
-__host__ __device__ constexpr int norm_sq_stride(int n) { return n / 4 + 4; }
-
-// The four lane chains of the squares in s_sq (lanes 0..3 of wave 0), then
-// lane 0 combines them with the tail and returns the scale in s_scale.
-// 32 terms are added while the next 32 are read from LDS.
-template <bool RMS>
-__device__ __forceinline__ void norm_scale(const float* s_sq, int st, int vq, int n,
-                                           const float* s_tail, float eps, float* s_part,
-                                           float* s_scale) {
-#pragma clang fp contract(off)
-    const int tid = threadIdx.x;
-    if (tid < 4) {
-        // two buffers of 32 terms take turns (no register copies between
-        // the dependent adds): one is added while the other is read
-        const float* t = s_sq + tid * st;
-        float acc = 0.0f;
-        int i = 0;
-        if (vq >= 64) {
-            float4 A[8], B[8];
-#define SLM_LOAD32(buf, off)                                                              \
-    _Pragma("unroll") for (int k = 0; k < 8; ++k) buf[k] =                                \
-        *reinterpret_cast<const float4*>(t + (off) + 4 * k)
-#define SLM_ADD32(buf)                                                                    \
-    _Pragma("unroll") for (int k = 0; k < 8; ++k) {                                       \
-        acc = acc + buf[k].x;                                                             \
-        acc = acc + buf[k].y;                                                             \
-        acc = acc + buf[k].z;                                                             \
-        acc = acc + buf[k].w;                                                             \
-    }
-            SLM_LOAD32(A, 0);
-            for (; i + 96 <= vq; i += 64) {  // A holds terms [i, i + 32)
-                // the scheduling barriers keep each read group where it is:
-                // hoisting a read above the adds of the buffer it refills
-                // would make the compiler copy registers between the adds
-                SLM_LOAD32(B, i + 32);
-                __builtin_amdgcn_sched_barrier(0);
-                SLM_ADD32(A);
-                __builtin_amdgcn_sched_barrier(0);
-                SLM_LOAD32(A, i + 64);
-                __builtin_amdgcn_sched_barrier(0);
-                SLM_ADD32(B);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            if (i + 64 <= vq) {
-                SLM_LOAD32(B, i + 32);
-                SLM_ADD32(A);
-                SLM_ADD32(B);
-                i += 64;
-            } else {
-                SLM_ADD32(A);
-                i += 32;
-            }
-#undef SLM_LOAD32
-#undef SLM_ADD32
-        }
-        for (; i < vq; ++i) acc = acc + t[i];
-        s_part[tid] = acc;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (tid == 0) {
-        float s = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
-        for (int i = 0; i < n - 4 * vq; ++i) s = s + s_tail[i];
-        float scale;
-        if (RMS) {  // graph.rs:141-156
-            const float inv_n = __fdiv_rn(1.0f, (float)n);
-            const float mean = s * inv_n;
-            const float var = mean + eps;
-            scale = __fdiv_rn(1.0f, sqrt_rn(var));
-        } else {    // graph.rs:182-193
-            const float var = s + eps;
-            scale = __fdiv_rn(1.0f, sqrt_rn(var));
-        }
-        *s_scale = scale;
-    }
-}
-
 // Rows of n % 32 == 0: quad q of the workgroup owns blocks q, q + 64, ...
 // (lane part p: elements 8p..8p+7 of each) in both phases, so x and w are
 // loaded once, up front, and held in registers across the chain.
@@ -146,33 +69,9 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(NormArgs a) {
     const int nb = n / 32;
     const int passes = (nb + 63) / 64;
 
-    float4 xr[kNormMaxPasses][2], wr[kNormMaxPasses][2];
-#pragma unroll
-    for (int k = 0; k < kNormMaxPasses; ++k) {
-        if (k >= passes) break;  // uniform
-        const int blk = min((tid >> 2) + 64 * k, nb - 1);  // clamped; not stored past nb
-        const int e0 = 32 * blk + 8 * part;
-        xr[k][0] = ld4(x + e0);
-        xr[k][1] = ld4(x + e0 + 4);
-        if (RMS) {
-            wr[k][0] = ld4(a.w + e0);
-            wr[k][1] = ld4(a.w + e0 + 4);
-        }
-    }
-    // squares, transposed: element e = 32 blk + 8 part + j goes to chain
-    // j % 4 at position 8 blk + 2 part + j / 4
-#pragma unroll
-    for (int k = 0; k < kNormMaxPasses; ++k) {
-        if (k >= passes) break;
-        const int blk = (tid >> 2) + 64 * k;
-        if (blk < nb) {
-            const int i0 = 8 * blk + 2 * part;
-            const float v[8] = {xr[k][0].x, xr[k][0].y, xr[k][0].z, xr[k][0].w,
-                                xr[k][1].x, xr[k][1].y, xr[k][1].z, xr[k][1].w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s_sq[(j & 3) * st + i0 + (j >> 2)] = v[j] * v[j];
-        }
-    }
+    NormRow<kNormMaxPasses> r;
+    norm_row_load<kNormMaxPasses, RMS>(r, x, a.w, nb);
+    norm_row_squares(r, nb, s_sq);
     __syncthreads();
     norm_scale<RMS>(s_sq, st, vq, n, s_tail, a.eps, s_part, &s_scale);
     __syncthreads();
@@ -183,29 +82,15 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(NormArgs a) {
         if (k >= passes) break;
         const int blk = (tid >> 2) + 64 * k;
         if (blk >= nb) break;  // uniform over the quad
-        float v[8] = {xr[k][0].x, xr[k][0].y, xr[k][0].z, xr[k][0].w,
-                      xr[k][1].x, xr[k][1].y, xr[k][1].z, xr[k][1].w};
-        if (RMS) {
-            const float wv[8] = {wr[k][0].x, wr[k][0].y, wr[k][0].z, wr[k][0].w,
-                                 wr[k][1].x, wr[k][1].y, wr[k][1].z, wr[k][1].w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float nx = v[j] * scale;
-                v[j] = nx * wv[j];
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = v[j] * scale;
-        }
+        float4 f0, f1;
+        norm_row_values<kNormMaxPasses, RMS>(r, k, scale, &f0, &f1);
         const int e0 = 32 * blk + 8 * part;
         if (a.out) {
             float* o = a.out + (long)blockIdx.x * a.out_stride + e0;
-            *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
-            *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            *reinterpret_cast<float4*>(o) = f0;
+            *reinterpret_cast<float4*>(o + 4) = f1;
         }
-        if (a.q8.q)
-            store_q8_quad(a.q8, blockIdx.x, blk, part, make_float4(v[0], v[1], v[2], v[3]),
-                          make_float4(v[4], v[5], v[6], v[7]));
+        if (a.q8.q) store_q8_quad(a.q8, blockIdx.x, blk, part, f0, f1);
     }
 }
 

@@ -27,6 +27,7 @@
 
 #include "attn_common.h"
 #include "jit_math.h"
+#include "norm_common.h"
 #include "quant_common.h"
 #include "slm_internal.h"
 
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
     }
 }
 
-// ---- GEMV from pre-quantized activations (one token) ----
+// ---- GEMV of one token, activations quantized or normalized on the way ----
 //
 // The activation blocks come quantized (q [nb][32] i8, d and block sums
 // [nb]) from the producing kernel, so a workgroup has no quantization phase
@@ -311,21 +312,118 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
 // 64j + l), loading the weight blocks together with the matching activation
 // blocks kPrefetch chunks ahead, and advances the ordered sums chunk by chunk
 // as in gemv_q4_kernel.
+//
+// Or (NORM) the workgroup takes the f32 row the RMSNorm before the
+// projection reads (transformer.rs:411 and :448-454: rmsnorm, then the
+// projection quantizes its output) and normalizes it itself, with the
+// standalone norm kernel's operations in the same order, so the Q8_0 blocks
+// it quantizes into LDS carry the same bits: the row and the norm weights
+// are loaded and the squares written first, then waves 1-3 issue their
+// first weight chunks, so the weights stream in while wave 0 runs the four
+// reduction chains.  This takes the
+// norm's launch and its round trip through memory off the decode step.
+
+struct GemvAct {
+    const uint32_t* aq;  // [nb][8] quantized blocks, or
+    const float* ad;     // [nb]
+    const int* as;       // [nb]
+    const float* x;      // (NORM) the row to normalize, [nb * 32]
+    const float* w;      // (NORM) its RMSNorm weights
+    float eps;
+};
 
 struct GemvQ8Params {
     QMat m[3];
     int nmat;
     int tiles[3];        // kGemvRows-row tiles per matrix
-    const uint32_t* aq;  // [nb][8]
-    const float* ad;     // [nb]
-    const int* as;       // [nb]
+    GemvAct a;
     int nb;
 };
 
-template <int NBL>
+// LDS of a normalizing workgroup (dwords): the squares [4][norm_sq_stride],
+// then the quantized row q [nb][8], d [nb], sums [nb], then the reduction's
+// partials [4], tail [4] and scale.
+__host__ __device__ constexpr int gemv_norm_q_offset(int nb) {
+    return 4 * norm_sq_stride(32 * nb);
+}
+constexpr size_t gemv_norm_lds_bytes(int nb) {
+    return (size_t)(gemv_norm_q_offset(nb) + nb * 10 + 12) * 4;
+}
+
+// Waits for the norm weights of the row's passes: they are loaded with the
+// row but first read after the reduction, and a wait for them issued behind
+// the weight loads would wait for those too (loads complete in order).
+template <int KP>
+__device__ __forceinline__ void norm_row_wait_w(const NormRow<KP>& r, int nb) {
+    const int passes = (nb + 63) / 64;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+        if (k >= passes) break;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            asm volatile("" ::"v"(r.w[k][h].x), "v"(r.w[k][h].y), "v"(r.w[k][h].z),
+                         "v"(r.w[k][h].w));
+    }
+}
+
+// The reduction (wave 0) over the squares the workgroup has written to LDS
+// (after a barrier), then the normalized row quantized into LDS; ends at a
+// workgroup barrier.
+template <int KP, int T>
+__device__ __forceinline__ void norm_row_to_lds(const NormRow<KP>& r, int nb, float eps,
+                                                uint32_t* smem) {
+    float* s_sq = reinterpret_cast<float*>(smem);
+    uint32_t* s_q = smem + gemv_norm_q_offset(nb);
+    float* s_d = reinterpret_cast<float*>(s_q + nb * 8);
+    int* s_sum = reinterpret_cast<int*>(s_d + nb);
+    float* s_small = reinterpret_cast<float*>(s_sum + nb);
+    const int n = 32 * nb;
+    norm_scale<true, T>(s_sq, norm_sq_stride(n), n / 4, n, s_small + 4, eps, s_small,
+                        s_small + 8);
+    __syncthreads();
+    const float scale = s_small[8];
+    const int part = threadIdx.x & 3;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+        const int blk = (threadIdx.x >> 2) + 64 * k;
+        if (blk < nb) {  // uniform over the quad
+            float4 f0, f1;
+            norm_row_values<KP, true>(r, k, scale, &f0, &f1);
+            uint2 q;
+            uint16_t dbits;
+            int sum;
+            quantize_q8_quad(f0, f1, &q, &dbits, &sum);
+            *reinterpret_cast<uint2*>(s_q + blk * 8 + 2 * part) = q;
+            if (part == 0) {
+                s_d[blk] = h2f(dbits);
+                s_sum[blk] = sum;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Activation block b of a chunk: from the prefetched registers, or from the
+// workgroup's quantized row in LDS.
+struct ActBlock {
+    uint32_t a[8];
+    float d;
+    int s;
+};
+__device__ __forceinline__ ActBlock act_lds(const uint32_t* smem, int nb, int b) {
+    const uint32_t* s_q = smem + gemv_norm_q_offset(nb);
+    const uint4 a0 = *reinterpret_cast<const uint4*>(s_q + b * 8);
+    const uint4 a1 = *reinterpret_cast<const uint4*>(s_q + b * 8 + 4);
+    return ActBlock{{a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w},
+                    reinterpret_cast<const float*>(s_q + nb * 8)[b],
+                    reinterpret_cast<const int*>(s_q + nb * 9)[b]};
+}
+
+template <bool NORM, int NBL>
 __global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
 #pragma clang fp contract(off)
     __shared__ __align__(16) float s_t[4][kGemvRowsPerWave][kTermStride];
+    extern __shared__ __align__(16) uint32_t smem[];  // NORM: gemv_norm_lds_bytes(nb)
     const int nb = p.nb;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -337,6 +435,18 @@ __global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
     const QMat M = pick(p.m, m);
     const int rw = tile * kGemvRows + wave * kGemvRowsPerWave;
 
+    // (NORM) the row, its squares and its norm weights first; then waves
+    // 1-3 issue their first weight chunks while wave 0 runs the reduction,
+    // and wave 0 issues its own after it: a wave stalls issuing loads while
+    // the memory pipeline is full, which would hold up the reduction
+    NormRow<NBL> nr;
+    if constexpr (NORM) {
+        norm_row_load<NBL, true>(nr, p.a.x, p.a.w, nb);
+        norm_row_squares(nr, nb, reinterpret_cast<float*>(smem));
+        norm_row_wait_w(nr, nb);
+        __syncthreads();
+    }
+    __builtin_amdgcn_sched_barrier(0);
     uint4 a0[NBL], a1[NBL];
     float da[NBL];
     int as[NBL];
@@ -345,18 +455,30 @@ __global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
 #define SLM_GEMV_ISSUE(j)                                                                    \
     do {                                                                                     \
         const int b_ = min(kChunk * (j) + lane, nb - 1);                                     \
-        a0[j] = *reinterpret_cast<const uint4*>(p.aq + (long)b_ * 8);                        \
-        a1[j] = *reinterpret_cast<const uint4*>(p.aq + (long)b_ * 8 + 4);                    \
-        da[j] = p.ad[b_];                                                                    \
-        as[j] = p.as[b_];                                                                    \
+        if constexpr (!NORM) {                                                               \
+            a0[j] = *reinterpret_cast<const uint4*>(p.a.aq + (long)b_ * 8);                  \
+            a1[j] = *reinterpret_cast<const uint4*>(p.a.aq + (long)b_ * 8 + 4);              \
+            da[j] = p.a.ad[b_];                                                              \
+            as[j] = p.a.as[b_];                                                              \
+        }                                                                                    \
         _Pragma("unroll") for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {                    \
             const int r_ = min(rw + rr, M.rows - 1);                                         \
             wq[j][rr] = *reinterpret_cast<const uint4*>(M.qs + ((long)r_ * nb + b_) * 16);   \
             wd[j][rr] = M.d[(long)r_ * M.d_stride + b_];                                     \
         }                                                                                    \
     } while (0)
+    if (!NORM || wave != 0) {
 #pragma unroll
-    for (int j = 0; j < (kPrefetch < NBL ? kPrefetch : NBL); ++j) SLM_GEMV_ISSUE(j);
+        for (int j = 0; j < (kPrefetch < NBL ? kPrefetch : NBL); ++j) SLM_GEMV_ISSUE(j);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+        norm_row_to_lds<NBL, 32>(nr, nb, p.a.eps, smem);
+        if (wave == 0) {
+#pragma unroll
+            for (int j = 0; j < (kPrefetch < NBL ? kPrefetch : NBL); ++j) SLM_GEMV_ISSUE(j);
+        }
+    }
 
     float acc = 0.0f;
 #pragma unroll
@@ -365,12 +487,17 @@ __global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
         __builtin_amdgcn_sched_barrier(0);
         const int b0 = kChunk * j;
         if (b0 + lane < nb) {
-            const uint32_t a[8] = {a0[j].x, a0[j].y, a0[j].z, a0[j].w,
-                                   a1[j].x, a1[j].y, a1[j].z, a1[j].w};
+            ActBlock ab;
+            if constexpr (NORM) {
+                ab = act_lds(smem, nb, b0 + lane);
+            } else {
+                ab = ActBlock{{a0[j].x, a0[j].y, a0[j].z, a0[j].w,
+                               a1[j].x, a1[j].y, a1[j].z, a1[j].w}, da[j], as[j]};
+            }
 #pragma unroll
             for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
-                const int isum = block_dot(wq[j][rr], a, as[j]);
-                s_t[wave][rr][lane] = (float)isum * (h2f(wd[j][rr]) * da[j]);
+                const int isum = block_dot(wq[j][rr], ab.a, ab.s);
+                s_t[wave][rr][lane] = (float)isum * (h2f(wd[j][rr]) * ab.d);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -393,40 +520,55 @@ __global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
     }
 }
 
-// ---- gate and up from pre-quantized activations, SwiGLU fused ----
+// ---- gate and up of one token, SwiGLU fused ----
 //
 // FuseGraph::swiglu (graph.rs:131-139) reads the gate and up rows of the same
 // hidden index, so a workgroup takes 32 hidden rows of both matrices (wave w:
 // rows 8w..8w+7 of each, 16 row streams) and, once its ordered sums are done,
 // one quad forms act = silu(gate) * up for the 32 rows and quantizes them as
 // the one Q8_0 block the down projection reads (quantize_row_q8_0 of act).
-// Gate, up and act carry the same bits as the separate kernels give.
+// Gate, up and act carry the same bits as the separate kernels give.  The
+// activations come as in gemv_q8in_kernel: quantized, or (NORM) the FFN
+// RMSNorm's input row, normalized by the workgroup.
 
 constexpr int kSwRowsPerWave = 8;             // hidden rows per wave (of each matrix)
 constexpr int kSwRows = 4 * kSwRowsPerWave;   // hidden rows per workgroup: one Q8_0 block
 
 struct GemvSwigluParams {
     QMat gate, up;       // [hidden][nb]; out/res unused
-    const uint32_t* aq;  // [nb][8]
-    const float* ad;     // [nb]
-    const int* as;       // [nb]
+    GemvAct a;
     int nb;
     float* act;          // [hidden] f32, or nullptr
     Q8Out q8;            // act as Q8_0 blocks (one row of hidden / 32 blocks)
 };
 
-template <int NBL>
+template <bool NORM, int NBL>
 __global__ __launch_bounds__(256) void gemv_q8in_swiglu_kernel(GemvSwigluParams p) {
 #pragma clang fp contract(off)
     constexpr int R = 2 * kSwRowsPerWave;  // row streams per wave: gate rows, then up rows
+    // chunks in flight ahead of the sums.  Normalizing, the reduction runs
+    // while they stream in: rows of up to two chunks have both in flight
+    // (with the reduction's 16-term buffers this fits the 256 registers of
+    // two waves per SIMD, so all workgroups of a 14336-row FFN are
+    // resident); longer rows keep one ahead.
+    constexpr int PF = NORM && NBL > 2 ? 1 : kPrefetch;
     __shared__ __align__(16) float s_t[4][R][kTermStride];
     __shared__ float s_g[kSwRows], s_u[kSwRows];
+    extern __shared__ __align__(16) uint32_t smem[];  // NORM: gemv_norm_lds_bytes(nb)
     const int nb = p.nb;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int h0 = blockIdx.x * kSwRows;             // the workgroup's block of hidden rows
     const int hw = h0 + wave * kSwRowsPerWave;       // this wave's first row
 
+    NormRow<NBL> nr;  // (NORM) the row first, the weights around the reduction, as in
+    if constexpr (NORM) {  // gemv_q8in_kernel
+        norm_row_load<NBL, true>(nr, p.a.x, p.a.w, nb);
+        norm_row_squares(nr, nb, reinterpret_cast<float*>(smem));
+        norm_row_wait_w(nr, nb);
+        __syncthreads();
+    }
+    __builtin_amdgcn_sched_barrier(0);
     uint4 a0[NBL], a1[NBL];
     float da[NBL];
     int as[NBL];
@@ -435,10 +577,12 @@ __global__ __launch_bounds__(256) void gemv_q8in_swiglu_kernel(GemvSwigluParams 
 #define SLM_SW_ISSUE(j)                                                                      \
     do {                                                                                     \
         const int b_ = min(kChunk * (j) + lane, nb - 1);                                     \
-        a0[j] = *reinterpret_cast<const uint4*>(p.aq + (long)b_ * 8);                        \
-        a1[j] = *reinterpret_cast<const uint4*>(p.aq + (long)b_ * 8 + 4);                    \
-        da[j] = p.ad[b_];                                                                    \
-        as[j] = p.as[b_];                                                                    \
+        if constexpr (!NORM) {                                                               \
+            a0[j] = *reinterpret_cast<const uint4*>(p.a.aq + (long)b_ * 8);                  \
+            a1[j] = *reinterpret_cast<const uint4*>(p.a.aq + (long)b_ * 8 + 4);              \
+            da[j] = p.a.ad[b_];                                                              \
+            as[j] = p.a.as[b_];                                                              \
+        }                                                                                    \
         _Pragma("unroll") for (int rr = 0; rr < R; ++rr) {                                   \
             const QMat& M_ = rr < kSwRowsPerWave ? p.gate : p.up;                            \
             const long r_ = hw + (rr % kSwRowsPerWave);                                      \
@@ -446,22 +590,37 @@ __global__ __launch_bounds__(256) void gemv_q8in_swiglu_kernel(GemvSwigluParams 
             wd[j][rr] = M_.d[r_ * M_.d_stride + b_];                                         \
         }                                                                                    \
     } while (0)
+    if (!NORM || wave != 0) {
 #pragma unroll
-    for (int j = 0; j < (kPrefetch < NBL ? kPrefetch : NBL); ++j) SLM_SW_ISSUE(j);
+        for (int j = 0; j < (PF < NBL ? PF : NBL); ++j) SLM_SW_ISSUE(j);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+        norm_row_to_lds<NBL, 16>(nr, nb, p.a.eps, smem);
+        if (wave == 0) {
+#pragma unroll
+            for (int j = 0; j < (PF < NBL ? PF : NBL); ++j) SLM_SW_ISSUE(j);
+        }
+    }
 
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < NBL; ++j) {  // NBL = ceil(nb / kChunk)
-        if (j + kPrefetch < NBL) SLM_SW_ISSUE(j + kPrefetch);
+        if (j + PF < NBL) SLM_SW_ISSUE(j + PF);
         __builtin_amdgcn_sched_barrier(0);
         const int b0 = kChunk * j;
         if (b0 + lane < nb) {
-            const uint32_t a[8] = {a0[j].x, a0[j].y, a0[j].z, a0[j].w,
-                                   a1[j].x, a1[j].y, a1[j].z, a1[j].w};
+            ActBlock ab;
+            if constexpr (NORM) {
+                ab = act_lds(smem, nb, b0 + lane);
+            } else {
+                ab = ActBlock{{a0[j].x, a0[j].y, a0[j].z, a0[j].w,
+                               a1[j].x, a1[j].y, a1[j].z, a1[j].w}, da[j], as[j]};
+            }
 #pragma unroll
             for (int rr = 0; rr < R; ++rr) {
-                const int isum = block_dot(wq[j][rr], a, as[j]);
-                s_t[wave][rr][lane] = (float)isum * (h2f(wd[j][rr]) * da[j]);
+                const int isum = block_dot(wq[j][rr], ab.a, ab.s);
+                s_t[wave][rr][lane] = (float)isum * (h2f(wd[j][rr]) * ab.d);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -778,8 +937,24 @@ hipError_t launch_q4_gemv(const Q4Job* jobs, int njobs, const float* x, int nb, 
     return batch == 1 ? launch_gemv_nt<1>(p, grid, st) : launch_gemv_nt<4>(p, grid, st);
 }
 
-hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
-                             const int* as, int nb, hipStream_t st) {
+namespace {
+
+template <bool NORM, int NBL>
+hipError_t launch_gemv_q8_t(const GemvQ8Params& p, int grid, hipStream_t st) {
+    const size_t lds = NORM ? gemv_norm_lds_bytes(p.nb) : 0;
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(gemv_q8in_kernel<NORM, NBL>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((gemv_q8in_kernel<NORM, NBL>), dim3(grid), dim3(256), lds, st, p);
+    return hipGetLastError();
+}
+
+template <bool NORM>
+hipError_t launch_gemv_q8_any(const Q4Job* jobs, int njobs, const GemvAct& a, int nb,
+                              hipStream_t st) {
     if (njobs < 1 || njobs > 3 || nb < 1 || nb > 8 * kChunk) return hipErrorInvalidValue;
     GemvQ8Params p{};
     int grid = 0;
@@ -790,46 +965,89 @@ hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, c
         grid += p.tiles[i];
     }
     p.nmat = njobs;
-    p.aq = aq;
-    p.ad = ad;
-    p.as = as;
+    p.a = a;
     p.nb = nb;
     switch ((nb + kChunk - 1) / kChunk) {
-#define SLM_GEMV_Q8_CASE(n) \
-    case n: hipLaunchKernelGGL(gemv_q8in_kernel<n>, dim3(grid), dim3(256), 0, st, p); break;
-        SLM_GEMV_Q8_CASE(1) SLM_GEMV_Q8_CASE(2) SLM_GEMV_Q8_CASE(3) SLM_GEMV_Q8_CASE(4)
-        SLM_GEMV_Q8_CASE(5) SLM_GEMV_Q8_CASE(6) SLM_GEMV_Q8_CASE(7) SLM_GEMV_Q8_CASE(8)
-#undef SLM_GEMV_Q8_CASE
+        case 1: return launch_gemv_q8_t<NORM, 1>(p, grid, st);
+        case 2: return launch_gemv_q8_t<NORM, 2>(p, grid, st);
+        case 3: return launch_gemv_q8_t<NORM, 3>(p, grid, st);
+        case 4: return launch_gemv_q8_t<NORM, 4>(p, grid, st);
+        case 5: return launch_gemv_q8_t<NORM, 5>(p, grid, st);
+        case 6: return launch_gemv_q8_t<NORM, 6>(p, grid, st);
+        case 7: return launch_gemv_q8_t<NORM, 7>(p, grid, st);
+        case 8: return launch_gemv_q8_t<NORM, 8>(p, grid, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+template <bool NORM, int NBL>
+hipError_t launch_swiglu_t(const GemvSwigluParams& p, int grid, hipStream_t st) {
+    const size_t lds = NORM ? gemv_norm_lds_bytes(p.nb) : 0;
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(gemv_q8in_swiglu_kernel<NORM, NBL>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((gemv_q8in_swiglu_kernel<NORM, NBL>), dim3(grid), dim3(256), lds, st, p);
     return hipGetLastError();
 }
 
-hipError_t launch_q4_gemv_q8_swiglu(const Q4Job& gate, const Q4Job& up, const uint32_t* aq,
-                                    const float* ad, const int* as, int nb, float* act,
-                                    const Q8Out& q8, hipStream_t st) {
+template <bool NORM>
+hipError_t launch_swiglu_any(const Q4Job& gate, const Q4Job& up, const GemvAct& a, int nb,
+                             float* act, const Q8Out& q8, hipStream_t st) {
     const int hidden = gate.rows;
     if (up.rows != hidden || hidden % kSwRows || nb < 1 || nb > 8 * kChunk || !q8.q)
         return hipErrorInvalidValue;
     GemvSwigluParams p{};
     p.gate = QMat{gate.qs, gate.d, nullptr, nullptr, hidden, 0, q4_scale_stride(nb)};
     p.up = QMat{up.qs, up.d, nullptr, nullptr, hidden, 0, q4_scale_stride(nb)};
-    p.aq = aq;
-    p.ad = ad;
-    p.as = as;
+    p.a = a;
     p.nb = nb;
     p.act = act;
     p.q8 = q8;
     const int grid = hidden / kSwRows;
     switch ((nb + kChunk - 1) / kChunk) {
-#define SLM_SW_CASE(n) \
-    case n: hipLaunchKernelGGL(gemv_q8in_swiglu_kernel<n>, dim3(grid), dim3(256), 0, st, p); break;
-        SLM_SW_CASE(1) SLM_SW_CASE(2) SLM_SW_CASE(3) SLM_SW_CASE(4)
-        SLM_SW_CASE(5) SLM_SW_CASE(6) SLM_SW_CASE(7) SLM_SW_CASE(8)
-#undef SLM_SW_CASE
+        case 1: return launch_swiglu_t<NORM, 1>(p, grid, st);
+        case 2: return launch_swiglu_t<NORM, 2>(p, grid, st);
+        case 3: return launch_swiglu_t<NORM, 3>(p, grid, st);
+        case 4: return launch_swiglu_t<NORM, 4>(p, grid, st);
+        case 5: return launch_swiglu_t<NORM, 5>(p, grid, st);
+        case 6: return launch_swiglu_t<NORM, 6>(p, grid, st);
+        case 7: return launch_swiglu_t<NORM, 7>(p, grid, st);
+        case 8: return launch_swiglu_t<NORM, 8>(p, grid, st);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
+                             const int* as, int nb, hipStream_t st) {
+    return launch_gemv_q8_any<false>(jobs, njobs, GemvAct{aq, ad, as, nullptr, nullptr, 0.0f},
+                                     nb, st);
+}
+
+hipError_t launch_q4_gemv_norm(const Q4Job* jobs, int njobs, const float* x, const float* w,
+                               float eps, int nb, hipStream_t st) {
+    if (!x || !w) return hipErrorInvalidValue;
+    return launch_gemv_q8_any<true>(jobs, njobs, GemvAct{nullptr, nullptr, nullptr, x, w, eps},
+                                    nb, st);
+}
+
+hipError_t launch_q4_gemv_q8_swiglu(const Q4Job& gate, const Q4Job& up, const uint32_t* aq,
+                                    const float* ad, const int* as, int nb, float* act,
+                                    const Q8Out& q8, hipStream_t st) {
+    return launch_swiglu_any<false>(gate, up, GemvAct{aq, ad, as, nullptr, nullptr, 0.0f}, nb,
+                                    act, q8, st);
+}
+
+hipError_t launch_q4_gemv_norm_swiglu(const Q4Job& gate, const Q4Job& up, const float* x,
+                                      const float* w, float eps, int nb, float* act,
+                                      const Q8Out& q8, hipStream_t st) {
+    if (!x || !w) return hipErrorInvalidValue;
+    return launch_swiglu_any<true>(gate, up, GemvAct{nullptr, nullptr, nullptr, x, w, eps}, nb,
+                                   act, q8, st);
 }
 
 hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,

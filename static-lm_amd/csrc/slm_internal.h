@@ -123,6 +123,14 @@ struct Q8Out {
 hipError_t launch_q4_gemv_q8_swiglu(const Q4Job& gate, const Q4Job& up, const uint32_t* aq,
                                     const float* ad, const int* as, int nb, float* act,
                                     const Q8Out& q8, hipStream_t st);
+// The same two one-token projections from the f32 row x [nb * 32] that the
+// RMSNorm with weights w before them reads: every workgroup normalizes x
+// itself (the norm kernel's bits) and quantizes it into LDS.
+hipError_t launch_q4_gemv_norm(const Q4Job* jobs, int njobs, const float* x, const float* w,
+                               float eps, int nb, hipStream_t st);
+hipError_t launch_q4_gemv_norm_swiglu(const Q4Job& gate, const Q4Job& up, const float* x,
+                                      const float* w, float eps, int nb, float* act,
+                                      const Q8Out& q8, hipStream_t st);
 // any batch, from pre-quantized activations
 hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
                           int nb, int batch, hipStream_t st);

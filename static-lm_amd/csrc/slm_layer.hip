@@ -146,19 +146,20 @@ int slm_layer_forward_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t
     float* hb2 = hb + (size_t)n * hidden;        // up rows
     const bool one = n == 1;
 
-    // attention RMSNorm straight to Q8_0 blocks (transformer.rs:411 / 519-527)
-    {
-        Timed t(c, SLM_K_NORM);
-        hipError_t e = slm::launch_rmsnorm(x, s.dim, w->rms_att, n, s.dim, rms_eps, nullptr, 0,
-                                           q8_out(c, nb), st);
-        t.done();
-        if ((rc = run(c, e, "rmsnorm kernel launch"))) return rc;
-    }
-    // q, k, v (:413-417 / 530-561)
+    // attention RMSNorm (transformer.rs:411 / 519-527), then q, k, v
+    // (:413-417 / 530-561): for one token the projection normalizes the row
+    // itself, for a batch the norm writes Q8_0 blocks for the GEMM
     {
         const slm::Q4Job jobs[3] = {q4_job(w->wq, q), q4_job(w->wk, k), q4_job(w->wv, v)};
+        if (!one) {
+            Timed t(c, SLM_K_NORM);
+            hipError_t e = slm::launch_rmsnorm(x, s.dim, w->rms_att, n, s.dim, rms_eps, nullptr,
+                                               0, q8_out(c, nb), st);
+            t.done();
+            if ((rc = run(c, e, "rmsnorm kernel launch"))) return rc;
+        }
         Timed t(c, SLM_K_GEMM);
-        hipError_t e = one ? slm::launch_q4_gemv_q8(jobs, 3, c->q8_q, c->q8_d, c->q8_s, nb, st)
+        hipError_t e = one ? slm::launch_q4_gemv_norm(jobs, 3, x, w->rms_att, rms_eps, nb, st)
                            : slm::launch_q4_gemm(jobs, 3, c->q8_q, c->q8_d, nb, n, st);
         t.done();
         if ((rc = run(c, e, "q4 projection kernel launch"))) return rc;
@@ -173,23 +174,15 @@ int slm_layer_forward_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t
     }
     // x_mid = x + Wo . att (:445-446 / 595-605)
     if ((rc = project(c, w->wo, att, n, x_mid, x))) return rc;
-    // FFN RMSNorm to Q8_0 (:448-454 / 607-615)
-    {
-        Timed t(c, SLM_K_NORM);
-        hipError_t e = slm::launch_rmsnorm(x_mid, s.dim, w->rms_ffn, n, s.dim, rms_eps, nullptr,
-                                           0, q8_out(c, nb), st);
-        t.done();
-        if ((rc = run(c, e, "rmsnorm kernel launch"))) return rc;
-    }
     if (one) {
-        // gate and up with SwiGLU fused, act straight to Q8_0 blocks in the
-        // second activation buffer (:456-475)
+        // FFN RMSNorm (:448-454), gate and up, SwiGLU (:456-475) in one
+        // kernel, act straight to Q8_0 blocks in the second activation buffer
         {
             const slm::Q4Job gate = q4_job(w->w_gate, nullptr), up = q4_job(w->w_up, nullptr);
             const slm::Q8Out act{c->q8x_q, c->q8x_d, c->q8x_s, nbh, slm::q4_scale_stride(nbh)};
             Timed t(c, SLM_K_GEMM);
-            hipError_t e = slm::launch_q4_gemv_q8_swiglu(gate, up, c->q8_q, c->q8_d, c->q8_s, nb,
-                                                         nullptr, act, st);
+            hipError_t e = slm::launch_q4_gemv_norm_swiglu(gate, up, x_mid, w->rms_ffn, rms_eps,
+                                                           nb, nullptr, act, st);
             t.done();
             if ((rc = run(c, e, "q4 projection kernel launch"))) return rc;
         }
@@ -199,6 +192,14 @@ int slm_layer_forward_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t
         hipError_t e = slm::launch_q4_gemv_q8(&job, 1, c->q8x_q, c->q8x_d, c->q8x_s, nbh, st);
         t.done();
         return run(c, e, "q4 projection kernel launch");
+    }
+    // FFN RMSNorm to Q8_0 (:607-615)
+    {
+        Timed t(c, SLM_K_NORM);
+        hipError_t e = slm::launch_rmsnorm(x_mid, s.dim, w->rms_ffn, n, s.dim, rms_eps, nullptr,
+                                           0, q8_out(c, nb), st);
+        t.done();
+        if ((rc = run(c, e, "rmsnorm kernel launch"))) return rc;
     }
     // gate and up (:617-636)
     {

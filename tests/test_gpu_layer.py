@@ -191,7 +191,10 @@ BLOCK_SHAPES = [
     (64, 128, 4, 4, 40),          # the reference's MHA layer test shape
     (128, 256, 8, 2, 40),         # the reference's GQA layer test shape
     (576, 1536, 9, 3, 64),        # SmolLM2-135M
+    (2560, 1024, 20, 4, 40),      # rows of 80 blocks: a partial second chunk
     (4096, 14336, 32, 8, 40),     # Llama-3-8B
+    (8192, 512, 64, 8, 32),       # Llama-3-70B's width, four chunks
+    (12288, 256, 96, 8, 32),      # six chunks, above 64 KiB of LDS when normalizing
 ]
 # (start, n) calls in order: prefill, decode steps, a later prefill chunk,
 # small batches (n <= 4 take the MFMA GEMM), more decode
