@@ -42,6 +42,10 @@ HIP_FLAGS = [
     f"-I{REPO / 'include'}",
     f"-I{CSRC}",
 ]
+# per-source extras: the Q4_0 GEMM's MFMA results go straight to VGPRs (its
+# epilogue reads every one; accumulator registers would cost a
+# v_accvgpr_read per element)
+HIP_SOURCE_FLAGS = {"quant_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _run(cmd: list[str]) -> None:
@@ -61,7 +65,8 @@ def build_library(jobs: int = 4) -> Path:
     for src in HIP_SOURCES:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         objs.append(obj)
-        cmds.append([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([HIPCC, *HIP_FLAGS, *HIP_SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src),
+                     "-o", str(obj)])
     for src in CPP_SOURCES:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         objs.append(obj)

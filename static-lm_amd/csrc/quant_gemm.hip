@@ -655,10 +655,13 @@ __global__ __launch_bounds__(256) void gemv_q8in_swiglu_kernel(GemvSwigluParams 
 //
 // Workgroup tile 64 rows x 64 tokens, four waves of 32 x 32 (2 x 2 tiles of
 // v_mfma_i32_16x16x32_i8, one Q-block of K = 32 per instruction).  Lane l
-// feeds A[l%16][8*(l/16)..+7] = weights 8g..8g+7 of row l%16 (g = l/16: low
-// nibbles of bytes 0-7 / 8-15, then high nibbles of bytes 0-7 / 8-15) and
+// feeds A[l%16][8*(l/16)..+7] = weights 8g..8g+7 of row l%16 (g = l/16) and
 // B[8g..+7][l%16] = the same eight activations of token l%16, and holds
 // D[4g+j][l%16].  Per block each element gets acc = acc + float(D) * (dw*da).
+// The kernel is bound by that f32 epilogue (VALU), so everything else that
+// costs VALU is done once per workgroup at staging: the nibbles are widened
+// to i8 weights (in weight order, so a fragment is one 8-byte read) and the
+// weight scales to f32.
 
 struct GemmParams {
     QMat m[3];
@@ -680,16 +683,16 @@ __device__ __forceinline__ uint32_t nib_to_i8(uint32_t x) {
 }
 
 // LDS stage of the GEMM: kScaleChunk blocks of the workgroup's 64 weight rows
-// and 64 tokens.  Row strides are padded (36 and 68 dwords) so that the
-// 8-byte fragment reads of a half-wave (16 rows or tokens x 2 lane groups)
-// hit 64 different banks; scales are stored block-major so a lane's four
-// rows are one 8-byte read.
-constexpr int kAStride = 36;  // dwords per weight row: 8 blocks x 16 B + pad
+// (widened to i8) and 64 tokens.  Row strides are padded to 68 dwords so that
+// the 8-byte fragment reads of a half-wave (16 rows or tokens x 2 lane
+// groups) hit 64 different banks; scales are stored block-major so a lane's
+// four rows are one 16-byte read.
+constexpr int kAStride = 68;  // dwords per weight row: 8 blocks x 32 i8 + pad
 constexpr int kBStride = 68;  // dwords per token: 8 blocks x 32 B + pad
 struct GemmStage {
     uint32_t a[kGemmTile * kAStride];
     uint32_t b[kGemmTile * kBStride];
-    uint16_t dw[kScaleChunk][kGemmTile];
+    float dw[kScaleChunk][kGemmTile];
     float da[kScaleChunk][kGemmTile];
 };
 
@@ -744,24 +747,37 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
         else if (tid < 192)                                                              \
             rs = *reinterpret_cast<const uint4*>(dasrc + (b0));                          \
     } while (0)
+    // a block's 16 nibble bytes as its 32 i8 weights in order: byte k holds
+    // weight k (low nibble) and weight k + 16 (high nibble)
+    auto widen = [](const uint4 q, uint4* lo, uint4* hi) {
+        *lo = make_uint4(nib_to_i8(q.x & 0x0F0F0F0Fu), nib_to_i8(q.y & 0x0F0F0F0Fu),
+                         nib_to_i8(q.z & 0x0F0F0F0Fu), nib_to_i8(q.w & 0x0F0F0F0Fu));
+        *hi = make_uint4(nib_to_i8((q.x >> 4) & 0x0F0F0F0Fu), nib_to_i8((q.y >> 4) & 0x0F0F0F0Fu),
+                         nib_to_i8((q.z >> 4) & 0x0F0F0F0Fu), nib_to_i8((q.w >> 4) & 0x0F0F0F0Fu));
+    };
 #define SLM_GEMM_STORE_STAGE(S)                                                           \
     do {                                                                                  \
         const int kb0 = 2 * lsub;                                                         \
-        *reinterpret_cast<uint4*>(&(S).a[lrow * kAStride + kb0 * 4]) = ra0;               \
-        *reinterpret_cast<uint4*>(&(S).a[lrow * kAStride + kb0 * 4 + 4]) = ra1;           \
+        uint4 w0_, w1_;                                                                   \
+        widen(ra0, &w0_, &w1_);                                                           \
+        *reinterpret_cast<uint4*>(&(S).a[lrow * kAStride + kb0 * 8]) = w0_;               \
+        *reinterpret_cast<uint4*>(&(S).a[lrow * kAStride + kb0 * 8 + 4]) = w1_;           \
+        widen(ra1, &w0_, &w1_);                                                           \
+        *reinterpret_cast<uint4*>(&(S).a[lrow * kAStride + kb0 * 8 + 8]) = w0_;           \
+        *reinterpret_cast<uint4*>(&(S).a[lrow * kAStride + kb0 * 8 + 12]) = w1_;          \
         *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8]) = rb0;               \
         *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 4]) = rb1;           \
         *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 8]) = rb2;           \
         *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 12]) = rb3;          \
         if (tid < 64) {                                                                   \
-            (S).dw[0][tid] = (uint16_t)(rs.x & 0xFFFF);                                   \
-            (S).dw[1][tid] = (uint16_t)(rs.x >> 16);                                      \
-            (S).dw[2][tid] = (uint16_t)(rs.y & 0xFFFF);                                   \
-            (S).dw[3][tid] = (uint16_t)(rs.y >> 16);                                      \
-            (S).dw[4][tid] = (uint16_t)(rs.z & 0xFFFF);                                   \
-            (S).dw[5][tid] = (uint16_t)(rs.z >> 16);                                      \
-            (S).dw[6][tid] = (uint16_t)(rs.w & 0xFFFF);                                   \
-            (S).dw[7][tid] = (uint16_t)(rs.w >> 16);                                      \
+            (S).dw[0][tid] = h2f((uint16_t)(rs.x & 0xFFFF));                              \
+            (S).dw[1][tid] = h2f((uint16_t)(rs.x >> 16));                                 \
+            (S).dw[2][tid] = h2f((uint16_t)(rs.y & 0xFFFF));                              \
+            (S).dw[3][tid] = h2f((uint16_t)(rs.y >> 16));                                 \
+            (S).dw[4][tid] = h2f((uint16_t)(rs.z & 0xFFFF));                              \
+            (S).dw[5][tid] = h2f((uint16_t)(rs.z >> 16));                                 \
+            (S).dw[6][tid] = h2f((uint16_t)(rs.w & 0xFFFF));                              \
+            (S).dw[7][tid] = h2f((uint16_t)(rs.w >> 16));                                 \
         } else if (tid < 192) {                                                           \
             const int t_ = (tid - 64) >> 1, h_ = 4 * ((tid - 64) & 1);                    \
             (S).da[h_ + 0][t_] = __uint_as_float(rs.x);                                   \
@@ -771,10 +787,8 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
         }                                                                                 \
     } while (0)
 
-    // this wave's 32 x 32 quadrant and the lane's fragment coordinates
+    // this wave's 32 x 32 quadrant
     const int qr = (wave & 1) * 32, qt = (wave >> 1) * 32;
-    const int half = (g & 1) * 2;    // dword offset of this lane's 8 nibble bytes
-    const int shift = (g >> 1) * 4;  // low or high nibbles
 
     float acc[2][2][4];
 #pragma unroll
@@ -799,10 +813,8 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const uint2 w = *reinterpret_cast<const uint2*>(
-                    &S.a[(qr + 16 * s + lr) * kAStride + kb * 4 + half]);
-                const uint32_t lo = nib_to_i8((w.x >> shift) & 0x0F0F0F0Fu);
-                const uint32_t hi = nib_to_i8((w.y >> shift) & 0x0F0F0F0Fu);
-                af[s] = (long)(((uint64_t)hi << 32) | lo);
+                    &S.a[(qr + 16 * s + lr) * kAStride + kb * 8 + 2 * g]);
+                af[s] = (long)(((uint64_t)w.y << 32) | w.x);
                 const uint2 x = *reinterpret_cast<const uint2*>(
                     &S.b[(qt + 16 * s + lr) * kBStride + kb * 8 + 2 * g]);
                 bf[s] = (long)(((uint64_t)x.y << 32) | x.x);
@@ -814,14 +826,17 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
                 for (int ts = 0; ts < 2; ++ts)
                     d[rs2][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[rs2], bf[ts],
                                                                        v4i{0, 0, 0, 0}, 0, 0, 0);
+            // the scale products stay on the VALU: on the matrix cores (an
+            // f16 or f32 MFMA whose K = 0 slice holds the two scales, exact)
+            // the epilogue waits for them and the kernel ran slower
             float dw[2][4], da[2];
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const uint2 h = *reinterpret_cast<const uint2*>(&S.dw[kb][qr + 16 * s + 4 * g]);
-                dw[s][0] = h2f((uint16_t)(h.x & 0xFFFF));
-                dw[s][1] = h2f((uint16_t)(h.x >> 16));
-                dw[s][2] = h2f((uint16_t)(h.y & 0xFFFF));
-                dw[s][3] = h2f((uint16_t)(h.y >> 16));
+                const float4 h = *reinterpret_cast<const float4*>(&S.dw[kb][qr + 16 * s + 4 * g]);
+                dw[s][0] = h.x;
+                dw[s][1] = h.y;
+                dw[s][2] = h.z;
+                dw[s][3] = h.w;
                 da[s] = S.da[kb][qt + 16 * s + lr];
             }
 #pragma unroll

@@ -98,6 +98,29 @@ def test_gemm_bit_exact_with_scalar_reference(ctx, rows, cols, batch):
     assert rel.max() < 1e-5
 
 
+@pytest.mark.parametrize("batch", [1, 70])
+def test_gemm_scales_across_the_f16_range(ctx, batch):
+    """Rows and tokens scaled from 1e-7 to 1e3: weight and activation block
+    scales from f16 subnormals (below 6.1e-5) to large normals, and zero rows
+    and tokens (scale 0), all bit for bit."""
+    rows, cols = 192, 512
+    row_mag = np.float32(10.0) ** np.linspace(-7, 3, rows).astype(np.float32)
+    row_mag[::17] = 0.0
+    w = orc.quantize_q4_0(gen([35], (rows, cols)) * row_mag[:, None])
+    tok_mag = np.float32(10.0) ** np.linspace(-6, 4, batch).astype(np.float32)
+    x = gen([36, batch], (batch, cols)) * tok_mag[:, None]
+    if batch > 3:
+        x[3] = 0.0
+    with P.Q4Matrix(w, rows, cols) as W:
+        xd = dev(x)
+        out = torch.full((batch, rows), float("nan"), device="cuda")
+        ctx.gemm_q4_0_dev(W, xd.data_ptr(), batch, out.data_ptr())
+        ctx.sync()
+        got = out.cpu().numpy()
+    want = orc.gemm_q4_0_f32(w, x, batch, rows, cols)
+    assert_bitwise(got, want, f"gemm scales batch {batch}")
+
+
 def test_gemm_batch_zero_is_a_no_op_and_shapes_are_checked(ctx):
     w = weights(41, 64, 64)
     with P.Q4Matrix(w, 64, 64) as W:
