@@ -666,7 +666,7 @@ __global__ __launch_bounds__(256) void gemv_q8in_swiglu_kernel(GemvSwigluParams 
 struct GemmParams {
     QMat m[3];
     int nmat;
-    int tiles[3];          // 64-row tiles per matrix
+    int tiles[3];          // row tiles of the workgroup shape per matrix
     const uint32_t* aq;    // [batch][nb][8]
     const float* ad;       // [batch][d_stride]
     int nb;
@@ -674,7 +674,6 @@ struct GemmParams {
     int batch;
 };
 
-constexpr int kGemmTile = 64;
 constexpr int kScaleChunk = 8;  // blocks whose scales one 128-bit load covers
 
 // nibbles 0..15 -> weight - 8 as i8, four per dword
@@ -682,23 +681,41 @@ __device__ __forceinline__ uint32_t nib_to_i8(uint32_t x) {
     return (x + 0x78787878u) ^ 0x80808080u;
 }
 
-// LDS stage of the GEMM: kScaleChunk blocks of the workgroup's 64 weight rows
-// (widened to i8) and 64 tokens.  Row strides are padded to 68 dwords so that
+// LDS stage of the GEMM: kScaleChunk blocks of the workgroup's RT weight rows
+// (widened to i8) and TT tokens.  Row strides are padded to 68 dwords so that
 // the 8-byte fragment reads of a half-wave (16 rows or tokens x 2 lane
 // groups) hit 64 different banks; scales are stored block-major so a lane's
 // four rows are one 16-byte read.
 constexpr int kAStride = 68;  // dwords per weight row: 8 blocks x 32 i8 + pad
 constexpr int kBStride = 68;  // dwords per token: 8 blocks x 32 B + pad
+template <int RT, int TT>
 struct GemmStage {
-    uint32_t a[kGemmTile * kAStride];
-    uint32_t b[kGemmTile * kBStride];
-    float dw[kScaleChunk][kGemmTile];
-    float da[kScaleChunk][kGemmTile];
+    uint32_t a[RT * kAStride];
+    uint32_t b[TT * kBStride];
+    float dw[kScaleChunk][RT];
+    float da[kScaleChunk][TT];
 };
 
-__global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
+// Workgroup shapes: WRW x WTW waves, each 32 rows x 16*NTS tokens.  64 x 64
+// (2 x 2 waves of 32 x 32) for small batches; 128 x 128 (4 x 2 waves of
+// 32 x 64) from 128 tokens, where each lane's 32 outputs share the block's
+// fragment and scale reads twice as widely (the loop's VALU cost per output
+// element and block falls from ~5.6 to ~4.9 ops, against the epilogue's 4).
+template <int WRW, int WTW, int NTS>
+struct GemmShape {
+    static constexpr int NW = WRW * WTW;
+    static constexpr int NT = 64 * NW;
+    static constexpr int RT = 32 * WRW;       // rows per workgroup
+    static constexpr int TT = 16 * NTS * WTW;  // tokens per workgroup
+    static_assert(RT == NT / 4 && TT == NT / 4, "one row and one token per thread quad");
+};
+
+template <int WRW, int WTW, int NTS>
+__global__ __launch_bounds__(64 * WRW * WTW) void gemm_q4_mfma_kernel(GemmParams p) {
 #pragma clang fp contract(off)
-    __shared__ __align__(16) GemmStage st[2];
+    using Sh = GemmShape<WRW, WTW, NTS>;
+    constexpr int RT = Sh::RT, TT = Sh::TT;
+    __shared__ __align__(16) GemmStage<RT, TT> st[2];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -706,7 +723,7 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
     const int g = lane >> 4;
 
     // workgroup -> (matrix, row tile, token tile); token tiles vary fastest
-    const int n_tt = (p.batch + kGemmTile - 1) / kGemmTile;
+    const int n_tt = (p.batch + TT - 1) / TT;
     int rt = blockIdx.x / n_tt;
     const int tt = blockIdx.x - rt * n_tt;
     int m = 0;
@@ -717,19 +734,20 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
     const QMat M = m == 0 ? p.m[0] : (m == 1 ? p.m[1] : p.m[2]);
     const int nb = p.nb;
     const int ds = p.d_stride;
-    const int wr0 = rt * kGemmTile;  // workgroup's first row / token
-    const int wt0 = tt * kGemmTile;
+    const int wr0 = rt * RT;  // workgroup's first row / token
+    const int wt0 = tt * TT;
 
     // Stage loads, all 16 bytes wide and coalesced, addresses clamped into
     // the buffers (rows / tokens / blocks past the end are never used):
     //   nibbles: thread -> (row tid/4, blocks 2*(tid%4), +1)
     //   activations: thread -> (token tid/4, blocks 2*(tid%4), +1)
-    //   weight scales: threads 0..63 -> row; activation scales: 64..191.
+    //   weight scales: threads 0..RT-1 -> row; activation scales: the next
+    //   2*TT threads, half a token's eight each.
     const int lrow = tid >> 2, lsub = tid & 3;
     const uint8_t* asrc = M.qs + (long)min(wr0 + lrow, M.rows - 1) * nb * 16;
     const uint32_t* bsrc = p.aq + (long)min(wt0 + lrow, p.batch - 1) * nb * 8;
-    const uint16_t* dwsrc = M.d + (long)min(wr0 + (tid & 63), M.rows - 1) * ds;
-    const int sidx = max(tid - 64, 0);  // threads 64..191 load activation scales
+    const uint16_t* dwsrc = M.d + (long)min(wr0 + min(tid, RT - 1), M.rows - 1) * ds;
+    const int sidx = min(max(tid - RT, 0), 2 * TT - 1);
     const float* dasrc = p.ad + (long)min(wt0 + (sidx >> 1), p.batch - 1) * ds + 4 * (sidx & 1);
     uint4 ra0, ra1, rb0, rb1, rb2, rb3, rs;
 #define SLM_GEMM_LOAD_STAGE(b0)                                                          \
@@ -742,9 +760,9 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
         rb1 = *reinterpret_cast<const uint4*>(bsrc + (long)blk0 * 8 + 4);                \
         rb2 = *reinterpret_cast<const uint4*>(bsrc + (long)blk1 * 8);                    \
         rb3 = *reinterpret_cast<const uint4*>(bsrc + (long)blk1 * 8 + 4);                \
-        if (tid < 64)                                                                    \
+        if (tid < RT)                                                                    \
             rs = *reinterpret_cast<const uint4*>(dwsrc + (b0));                          \
-        else if (tid < 192)                                                              \
+        else if (tid < RT + 2 * TT)                                                      \
             rs = *reinterpret_cast<const uint4*>(dasrc + (b0));                          \
     } while (0)
     // a block's 16 nibble bytes as its 32 i8 weights in order: byte k holds
@@ -769,7 +787,7 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
         *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 4]) = rb1;           \
         *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 8]) = rb2;           \
         *reinterpret_cast<uint4*>(&(S).b[lrow * kBStride + kb0 * 8 + 12]) = rb3;          \
-        if (tid < 64) {                                                                   \
+        if (tid < RT) {                                                                   \
             (S).dw[0][tid] = h2f((uint16_t)(rs.x & 0xFFFF));                              \
             (S).dw[1][tid] = h2f((uint16_t)(rs.x >> 16));                                 \
             (S).dw[2][tid] = h2f((uint16_t)(rs.y & 0xFFFF));                              \
@@ -778,8 +796,8 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
             (S).dw[5][tid] = h2f((uint16_t)(rs.z >> 16));                                 \
             (S).dw[6][tid] = h2f((uint16_t)(rs.w & 0xFFFF));                              \
             (S).dw[7][tid] = h2f((uint16_t)(rs.w >> 16));                                 \
-        } else if (tid < 192) {                                                           \
-            const int t_ = (tid - 64) >> 1, h_ = 4 * ((tid - 64) & 1);                    \
+        } else if (tid < RT + 2 * TT) {                                                   \
+            const int t_ = (tid - RT) >> 1, h_ = 4 * ((tid - RT) & 1);                    \
             (S).da[h_ + 0][t_] = __uint_as_float(rs.x);                                   \
             (S).da[h_ + 1][t_] = __uint_as_float(rs.y);                                   \
             (S).da[h_ + 2][t_] = __uint_as_float(rs.z);                                   \
@@ -787,14 +805,14 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
         }                                                                                 \
     } while (0)
 
-    // this wave's 32 x 32 quadrant
-    const int qr = (wave & 1) * 32, qt = (wave >> 1) * 32;
+    // this wave's 32 rows x 16*NTS tokens
+    const int qr = (wave % WRW) * 32, qt = (wave / WRW) * (16 * NTS);
 
-    float acc[2][2][4];
+    float acc[2][NTS][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < NTS; ++b)
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[a][b][j] = 0.0f;
 
@@ -804,32 +822,35 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
     for (int sg = 0; sg < n_stages; ++sg) {
         __syncthreads();  // stage sg is in st[sg & 1]; st[(sg+1) & 1] is free
         if (sg + 1 < n_stages) SLM_GEMM_LOAD_STAGE((sg + 1) * kScaleChunk);
-        const GemmStage& S = st[sg & 1];
+        const GemmStage<RT, TT>& S = st[sg & 1];
         const int b0 = sg * kScaleChunk;
 #pragma unroll
         for (int kb = 0; kb < kScaleChunk; ++kb) {
             if (b0 + kb >= nb) break;  // uniform
-            long af[2], bf[2];
+            long af[2], bf[NTS];
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const uint2 w = *reinterpret_cast<const uint2*>(
                     &S.a[(qr + 16 * s + lr) * kAStride + kb * 8 + 2 * g]);
                 af[s] = (long)(((uint64_t)w.y << 32) | w.x);
+            }
+#pragma unroll
+            for (int s = 0; s < NTS; ++s) {
                 const uint2 x = *reinterpret_cast<const uint2*>(
                     &S.b[(qt + 16 * s + lr) * kBStride + kb * 8 + 2 * g]);
                 bf[s] = (long)(((uint64_t)x.y << 32) | x.x);
             }
-            v4i d[2][2];
+            v4i d[2][NTS];
 #pragma unroll
             for (int rs2 = 0; rs2 < 2; ++rs2)
 #pragma unroll
-                for (int ts = 0; ts < 2; ++ts)
+                for (int ts = 0; ts < NTS; ++ts)
                     d[rs2][ts] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[rs2], bf[ts],
                                                                        v4i{0, 0, 0, 0}, 0, 0, 0);
             // the scale products stay on the VALU: on the matrix cores (an
             // f16 or f32 MFMA whose K = 0 slice holds the two scales, exact)
             // the epilogue waits for them and the kernel ran slower
-            float dw[2][4], da[2];
+            float dw[2][4], da[NTS];
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const float4 h = *reinterpret_cast<const float4*>(&S.dw[kb][qr + 16 * s + 4 * g]);
@@ -837,12 +858,13 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
                 dw[s][1] = h.y;
                 dw[s][2] = h.z;
                 dw[s][3] = h.w;
-                da[s] = S.da[kb][qt + 16 * s + lr];
             }
+#pragma unroll
+            for (int s = 0; s < NTS; ++s) da[s] = S.da[kb][qt + 16 * s + lr];
 #pragma unroll
             for (int rs2 = 0; rs2 < 2; ++rs2)
 #pragma unroll
-                for (int ts = 0; ts < 2; ++ts)
+                for (int ts = 0; ts < NTS; ++ts)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const float sc = dw[rs2][j] * da[ts];
@@ -855,7 +877,7 @@ __global__ __launch_bounds__(256) void gemm_q4_mfma_kernel(GemmParams p) {
 #pragma unroll
     for (int rs2 = 0; rs2 < 2; ++rs2)
 #pragma unroll
-        for (int ts = 0; ts < 2; ++ts) {
+        for (int ts = 0; ts < NTS; ++ts) {
             const int t = wt0 + qt + 16 * ts + lr;
             if (t >= p.batch) continue;
 #pragma unroll
@@ -1035,6 +1057,31 @@ hipError_t launch_swiglu_any(const Q4Job& gate, const Q4Job& up, const GemvAct& 
     }
 }
 
+template <int WRW, int WTW, int NTS>
+hipError_t launch_gemm_t(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
+                         int nb, int batch, hipStream_t st) {
+    using Sh = GemmShape<WRW, WTW, NTS>;
+    GemmParams p{};
+    long tiles = 0;
+    for (int i = 0; i < njobs; ++i) {
+        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].res, jobs[i].rows,
+                      jobs[i].out_stride, q4_scale_stride(nb)};
+        p.tiles[i] = (jobs[i].rows + Sh::RT - 1) / Sh::RT;
+        tiles += p.tiles[i];
+    }
+    p.nmat = njobs;
+    p.aq = aq;
+    p.ad = ad;
+    p.nb = nb;
+    p.d_stride = q4_scale_stride(nb);
+    p.batch = batch;
+    const long n_tt = (batch + Sh::TT - 1) / Sh::TT;
+    if (tiles * n_tt > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemm_q4_mfma_kernel<WRW, WTW, NTS>), dim3((unsigned)(tiles * n_tt)),
+                       dim3(Sh::NT), 0, st, p);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
@@ -1068,24 +1115,8 @@ hipError_t launch_q4_gemv_norm_swiglu(const Q4Job& gate, const Q4Job& up, const 
 hipError_t launch_q4_gemm(const Q4Job* jobs, int njobs, const uint32_t* aq, const float* ad,
                           int nb, int batch, hipStream_t st) {
     if (njobs < 1 || njobs > 3 || batch < 1) return hipErrorInvalidValue;
-    GemmParams p{};
-    long tiles = 0;
-    for (int i = 0; i < njobs; ++i) {
-        p.m[i] = QMat{jobs[i].qs, jobs[i].d, jobs[i].out, jobs[i].res, jobs[i].rows,
-                      jobs[i].out_stride, q4_scale_stride(nb)};
-        p.tiles[i] = (jobs[i].rows + kGemmTile - 1) / kGemmTile;
-        tiles += p.tiles[i];
-    }
-    p.nmat = njobs;
-    p.aq = aq;
-    p.ad = ad;
-    p.nb = nb;
-    p.d_stride = q4_scale_stride(nb);
-    p.batch = batch;
-    const long n_tt = (batch + kGemmTile - 1) / kGemmTile;
-    if (tiles * n_tt > 0x7FFFFFFF) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemm_q4_mfma_kernel, dim3((unsigned)(tiles * n_tt)), dim3(256), 0, st, p);
-    return hipGetLastError();
+    return batch >= 128 ? launch_gemm_t<4, 2, 4>(jobs, njobs, aq, ad, nb, batch, st)
+                        : launch_gemm_t<2, 2, 2>(jobs, njobs, aq, ad, nb, batch, st);
 }
 
 }  // namespace slm

@@ -77,6 +77,9 @@ GEMM_CASES = [
     (288, 288, 17),     # ragged row and token tiles
     (4096, 4096, 64),
     (320, 8192, 100),
+    (288, 288, 128),    # the 128 x 128 workgroups from 128 tokens: ragged row tile
+    (1024, 4096, 300),  # ragged token tile
+    (96, 16384, 130),   # nb 512 with the wide workgroups
 ]
 
 
@@ -98,7 +101,7 @@ def test_gemm_bit_exact_with_scalar_reference(ctx, rows, cols, batch):
     assert rel.max() < 1e-5
 
 
-@pytest.mark.parametrize("batch", [1, 70])
+@pytest.mark.parametrize("batch", [1, 70, 150])
 def test_gemm_scales_across_the_f16_range(ctx, batch):
     """Rows and tokens scaled from 1e-7 to 1e3: weight and activation block
     scales from f16 subnormals (below 6.1e-5) to large normals, and zero rows
