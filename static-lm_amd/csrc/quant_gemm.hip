@@ -320,8 +320,8 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
 // it quantizes into LDS carry the same bits: the row and the norm weights
 // are loaded and the squares written first, then waves 1-3 issue their
 // first weight chunks, so the weights stream in while wave 0 runs the four
-// reduction chains.  This takes the
-// norm's launch and its round trip through memory off the decode step.
+// reduction chains.  This takes the norm's launch and its round trip through
+// memory off the decode step.
 
 struct GemvAct {
     const uint32_t* aq;  // [nb][8] quantized blocks, or
