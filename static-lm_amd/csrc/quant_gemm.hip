@@ -35,6 +35,15 @@ namespace slm {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// A token's GEMV reads each weight once: nontemporal loads stream them past
+// the caches (measured 6% faster for the 66 MB gate/up GEMV; the GEMM, which
+// reuses weights across token tiles, keeps plain loads).
+__device__ __forceinline__ uint4 ldq_stream(const uint8_t* p) {
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // ---- standalone quantize_row_q8_0: 34-byte BlockQ8_0 output ----
 // Four lanes per block (coalesced 32-byte reads per lane).
@@ -232,8 +241,8 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvParams p) {
         const int b_ = min(kChunk * (j) + lane, nb - 1);                                     \
         _Pragma("unroll") for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {                    \
             const int r_ = min(rw + rr, M.rows - 1);                                         \
-            wq[j][rr] = *reinterpret_cast<const uint4*>(M.qs + ((long)r_ * nb + b_) * 16);   \
-            wd[j][rr] = M.d[(long)r_ * M.d_stride + b_];                                     \
+            wq[j][rr] = ldq_stream(M.qs + ((long)r_ * nb + b_) * 16);                        \
+            wd[j][rr] = __builtin_nontemporal_load(M.d + (long)r_ * M.d_stride + b_);        \
         }                                                                                    \
     } while (0)
 #pragma unroll
@@ -463,8 +472,8 @@ __global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
         }                                                                                    \
         _Pragma("unroll") for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {                    \
             const int r_ = min(rw + rr, M.rows - 1);                                         \
-            wq[j][rr] = *reinterpret_cast<const uint4*>(M.qs + ((long)r_ * nb + b_) * 16);   \
-            wd[j][rr] = M.d[(long)r_ * M.d_stride + b_];                                     \
+            wq[j][rr] = ldq_stream(M.qs + ((long)r_ * nb + b_) * 16);                        \
+            wd[j][rr] = __builtin_nontemporal_load(M.d + (long)r_ * M.d_stride + b_);        \
         }                                                                                    \
     } while (0)
     if (!NORM || wave != 0) {
@@ -586,8 +595,8 @@ __global__ __launch_bounds__(256) void gemv_q8in_swiglu_kernel(GemvSwigluParams 
         _Pragma("unroll") for (int rr = 0; rr < R; ++rr) {                                   \
             const QMat& M_ = rr < kSwRowsPerWave ? p.gate : p.up;                            \
             const long r_ = hw + (rr % kSwRowsPerWave);                                      \
-            wq[j][rr] = *reinterpret_cast<const uint4*>(M_.qs + (r_ * nb + b_) * 16);        \
-            wd[j][rr] = M_.d[r_ * M_.d_stride + b_];                                         \
+            wq[j][rr] = ldq_stream(M_.qs + (r_ * nb + b_) * 16);                             \
+            wd[j][rr] = __builtin_nontemporal_load(M_.d + r_ * M_.d_stride + b_);            \
         }                                                                                    \
     } while (0)
     if (!NORM || wave != 0) {
