@@ -442,6 +442,59 @@ def bench_layer(torch, P, steps: int) -> dict:
     return out
 
 
+VOCAB = 128256  # Llama-3 vocabulary
+
+
+def bench_model(torch, P, n_layers: int = 32, prompt_len: int = 512, gen: int = 64) -> dict:
+    """The whole model on the device (slm_model_prefill_dev,
+    slm_model_generate_dev): Llama-3-8B shape (32 layers, dim 4096, 32/8 heads,
+    hidden 14336, vocabulary 128256) with random Q4_0 weights, a 512-token
+    prompt, then greedy decode of 64 tokens (each token read back to the host,
+    as the reference's generate returns it)."""
+    rng = np.random.default_rng(29)
+    msl = prompt_len + gen + 1
+    stream = torch.cuda.current_stream()
+    ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, msl, n_layers, THETA)
+    ctx.set_stream(stream.cuda_stream)
+    lws, norm = make_layers(torch, P, rng, n_layers)
+    emb_host = random_q4_blocks(rng, VOCAB, DIM)
+    emb = P.Q4Matrix(emb_host, VOCAB, DIM)
+    head = P.Q4Matrix(emb_host, VOCAB, DIM)  # an untied output matrix of its own
+    mw = P.ModelWeights(emb, lws, norm.data_ptr(), head)
+    prompt = rng.integers(0, VOCAB, prompt_len).astype(np.int32)
+    ctx.model_generate_dev(mw, 1e-5, prompt[:32], 2)  # warm-up
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    ctx.model_prefill_dev(mw, 1e-5, prompt, 0)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+    walls = {}
+    for n_out in (1, gen):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks = ctx.model_generate_dev(mw, 1e-5, prompt, n_out)
+        walls[n_out] = time.perf_counter() - t0
+        assert len(toks) == n_out
+    per_token = (walls[gen] - walls[1]) / (gen - 1)
+    token_bytes = n_layers * layer_weight_bytes() + VOCAB * DIM // 32 * 18
+    ctx.close()
+    for lw in lws:
+        lw.close()
+    emb.close()
+    head.close()
+    del norm
+    return {
+        "workload": f"model forward on device, Llama-3-8B shape ({n_layers} layers, vocab {VOCAB}), "
+                    f"random Q4_0 weights: {prompt_len}-token prompt, greedy decode of {gen} tokens",
+        "prefill_ms": prefill_ms, "prefill_tokens_per_s": prompt_len / (prefill_ms / 1e3),
+        "decode_ms_per_token": per_token * 1e3, "decode_tokens_per_s": 1.0 / per_token,
+        "decode_weight_bytes_per_token": token_bytes,
+        "decode_weight_gbs": token_bytes / per_token / 1e9,
+    }
+
+
 def bench_decode_131k(torch, P) -> dict:
     pre, steps = 131072, 64
     msl = pre + steps
@@ -601,6 +654,9 @@ def main() -> int:
     ap.add_argument("--layer-only", action="store_true",
                     help="only the whole transformer block (decode and prefill); prints its "
                          "own JSON line, not the headline one")
+    ap.add_argument("--model-only", action="store_true",
+                    help="only the whole model (prefill and greedy decode, Llama-3-8B shape); "
+                         "prints its own JSON line, not the headline one")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB: a plain "
                          "copy kernel of known size that scales rocprofv3 byte counters")
@@ -641,6 +697,13 @@ def main() -> int:
         print(json.dumps(bl))
         return 0
 
+    if args.model_only:
+        bm = bench_model(torch, P)
+        log(f"model: prefill {bm['prefill_tokens_per_s']:.0f} tokens/s, decode "
+            f"{bm['decode_tokens_per_s']:.1f} tokens/s ({bm['decode_ms_per_token']:.2f} ms/token)")
+        print(json.dumps(bm))
+        return 0
+
     if args.xb_only:
         bx = bench_block_xb(torch, P, max(3, args.steps // 5))
         print(json.dumps(bx))
@@ -675,6 +738,10 @@ def main() -> int:
             f"{bx['prefill_xb_4k']['ms']:.3f} ms (GEMM {bx['prefill_xb_4k']['gemm_ms']:.3f} ms)")
         log("transformer block")
         blk = bench_layer(torch, P, max(3, args.steps // 5))
+        log("model")
+        bm = bench_model(torch, P)
+        log(f"model: prefill {bm['prefill_tokens_per_s']:.0f} tokens/s, decode "
+            f"{bm['decode_tokens_per_s']:.1f} tokens/s ({bm['decode_ms_per_token']:.2f} ms/token)")
         log("calibration")
         cal_mfma = P.calibrate_mfma_f32(iters=20000)
         cal_nt = P.calibrate_hbm_read(4 << 30, nontemporal=True)
@@ -703,6 +770,7 @@ def main() -> int:
             "configs": wl,
             **bx,
             "transformer_block": blk,
+            "model": bm,
         }
     cpu = None
     if args.cpu_seconds > 0:
