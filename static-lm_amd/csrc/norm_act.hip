@@ -242,6 +242,7 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t* qs, cons
 // lower index, and logits[0] being NaN short-cuts to 0.
 
 constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxBatch = 32;
 
 __device__ __forceinline__ void argmax_merge(float& v, int& i, float v2, int i2) {
     if (i2 < 0) return;
@@ -255,12 +256,22 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, 
                                                                 int32_t* out) {
     __shared__ float s_v[kArgmaxThreads / 64];
     __shared__ int s_i[kArgmaxThreads / 64];
+    // rounds of kArgmaxBatch loads per thread, all in flight before any is
+    // compared: one memory latency per round, not per element
     float bv = 0.0f;
     int bi = -1;
-    for (int e = threadIdx.x; e < n; e += kArgmaxThreads) {
-        const float v = x[e];
-        if (v != v) continue;
-        argmax_merge(bv, bi, v, e);
+    for (int base = 0; base < n; base += kArgmaxThreads * kArgmaxBatch) {
+        float v[kArgmaxBatch];
+#pragma unroll
+        for (int u = 0; u < kArgmaxBatch; ++u) {
+            const int e = base + u * kArgmaxThreads + (int)threadIdx.x;
+            v[u] = e < n ? x[e] : __builtin_nanf("");
+        }
+#pragma unroll
+        for (int u = 0; u < kArgmaxBatch; ++u) {
+            if (v[u] != v[u]) continue;  // NaN, or past the end
+            argmax_merge(bv, bi, v[u], base + u * kArgmaxThreads + (int)threadIdx.x);
+        }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {

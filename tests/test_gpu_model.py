@@ -16,7 +16,7 @@ import pytest
 
 from oracle import py_oracle as orc
 from slm_testlib import gen, load_product
-from test_oracle_layer import ref_model
+from test_oracle_layer import quantize_matrix, ref_model
 
 P = load_product()
 pytestmark = pytest.mark.gpu
@@ -225,3 +225,43 @@ def test_larger_model_prefill_matches_token_by_token():
             assert out == manual
     finally:
         dm.close()
+
+
+def test_argmax_first_maximum_over_a_large_vocabulary():
+    """sample_argmax (transformer.rs:654-666) over 70001 logits, several rounds
+    of the argmax kernel's batched loads: the token is the first index of the
+    maximum of the logits the device returns, also when the maximal lm_head
+    row is copied to a higher index and to a lower one (exact ties)."""
+    cfg, w = ref_model()
+    vocab = 70001
+    nbytes = cfg.dim // 32 * 18
+    embd = quantize_matrix(vocab, cfg.dim, 0x0400)
+    head = quantize_matrix(vocab, cfg.dim, 0x0500).reshape(vocab, nbytes)
+
+    def run(lm_head):
+        mw = orc.ModelWeights(embd, w.layers, w.output_norm, lm_head.reshape(-1), vocab)
+        dm = DeviceModel(cfg, mw)
+        try:
+            with P.AttentionContext(cfg.dim, cfg.num_heads, cfg.num_kv_heads, cfg.max_seq_len,
+                                    2, 1e4) as c:
+                logits = dev(np.full(vocab, np.nan, np.float32))
+                nxt = c.model_forward_token_dev(dm.w, EPS, 3, 0, logits.data_ptr())
+                c.sync()
+                return nxt, logits.cpu().numpy()
+        finally:
+            dm.close()
+
+    nxt, lg = run(head)
+    m = int(np.argmax(lg))
+    log(f"vocab {vocab}: token {nxt}, max {lg[m]:.4f} at {m}")
+    assert np.isfinite(lg).all() and nxt == m
+    hi = vocab - 2 if m != vocab - 2 else vocab - 3
+    dup = head.copy()
+    dup[hi] = head[m]
+    nxt, lg = run(dup)
+    assert lg[hi] == lg[m] and nxt == m  # a tie goes to the lower index
+    if m > 0:
+        lo = m // 2
+        dup[lo] = head[m]
+        nxt, lg = run(dup)
+        assert lg[lo] == lg[m] and nxt == lo
