@@ -242,36 +242,28 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t* qs, cons
 // lower index, and logits[0] being NaN short-cuts to 0.
 
 constexpr int kArgmaxThreads = 1024;
-constexpr int kArgmaxBatch = 32;
 
-__device__ __forceinline__ void argmax_merge(float& v, int& i, float v2, int i2) {
-    if (i2 < 0) return;
-    if (i < 0 || v2 > v || (v2 == v && i2 < i)) {
-        v = v2;
-        i = i2;
-    }
-}
+// Over the per-workgroup parts of the lm_head projection (its epilogue keeps
+// each workgroup's best row): one round of loads, then the wave and
+// workgroup merges.
+constexpr int kArgmaxPartsPerThread = 16;
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, int n,
-                                                                int32_t* out) {
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_parts_kernel(const ArgmaxPart* parts,
+                                                                      int n_parts, const float* x,
+                                                                      int32_t* out) {
     __shared__ float s_v[kArgmaxThreads / 64];
     __shared__ int s_i[kArgmaxThreads / 64];
-    // rounds of kArgmaxBatch loads per thread, all in flight before any is
-    // compared: one memory latency per round, not per element
     float bv = 0.0f;
     int bi = -1;
-    for (int base = 0; base < n; base += kArgmaxThreads * kArgmaxBatch) {
-        float v[kArgmaxBatch];
+    for (int base = 0; base < n_parts; base += kArgmaxThreads * kArgmaxPartsPerThread) {
+        ArgmaxPart q[kArgmaxPartsPerThread];
 #pragma unroll
-        for (int u = 0; u < kArgmaxBatch; ++u) {
-            const int e = base + u * kArgmaxThreads + (int)threadIdx.x;
-            v[u] = e < n ? x[e] : __builtin_nanf("");
+        for (int u = 0; u < kArgmaxPartsPerThread; ++u) {
+            const int k = base + u * kArgmaxThreads + (int)threadIdx.x;
+            q[u] = k < n_parts ? parts[k] : ArgmaxPart{0.0f, -1};
         }
 #pragma unroll
-        for (int u = 0; u < kArgmaxBatch; ++u) {
-            if (v[u] != v[u]) continue;  // NaN, or past the end
-            argmax_merge(bv, bi, v[u], base + u * kArgmaxThreads + (int)threadIdx.x);
-        }
+        for (int u = 0; u < kArgmaxPartsPerThread; ++u) argmax_merge(bv, bi, q[u].v, q[u].i);
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -365,9 +357,11 @@ hipError_t launch_mean_pool(const float* rows, int n, int dim, float inv, float*
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float* x, int n, int32_t* out, hipStream_t st) {
-    if (n <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, st, x, n, out);
+hipError_t launch_argmax_parts(const ArgmaxPart* parts, int n_parts, const float* x, int32_t* out,
+                               hipStream_t st) {
+    if (n_parts <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_parts_kernel, dim3(1), dim3(kArgmaxThreads), 0, st, parts, n_parts,
+                       x, out);
     return hipGetLastError();
 }
 

@@ -73,4 +73,14 @@ __device__ __forceinline__ void store_q8_quad(const Q8Out& o, long row, int blk,
     }
 }
 
+// sample_argmax's order (transformer.rs:654-666) for a parallel scan: the
+// larger value wins, a tie goes to the lower index; i < 0 marks "none".
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float v2, int i2) {
+    if (i2 < 0) return;
+    if (i < 0 || v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
 }  // namespace slm

@@ -347,6 +347,7 @@ struct GemvQ8Params {
     int tiles[3];        // kGemvRows-row tiles per matrix
     GemvAct a;
     int nb;
+    ArgmaxPart* am;      // (one matrix) each workgroup's best row, or nullptr
 };
 
 // LDS of a normalizing workgroup (dwords): the squares [4][norm_sq_stride],
@@ -525,6 +526,28 @@ __global__ __launch_bounds__(256) void gemv_q8in_kernel(GemvQ8Params p) {
             // the residual_add JIT kernel, out[i] = a[i] + b[i] (graph.rs:157-164)
             if (M.res) acc = M.res[r] + acc;
             M.out[r] = acc;
+        }
+    }
+    if (p.am) {  // uniform: the first maximum of the workgroup's rows, NaN skipped
+        __shared__ float s_av[4];
+        __shared__ int s_ai[4];
+        float v = acc;
+        int i = rw + lane;
+        if (lane >= kGemvRowsPerWave || i >= M.rows || v != v) i = -1;
+#pragma unroll
+        for (int off = 1; off < kGemvRowsPerWave; off <<= 1) {
+            const float v2 = __shfl_xor(v, off);
+            const int i2 = __shfl_xor(i, off);
+            argmax_merge(v, i, v2, i2);
+        }
+        if (lane == 0) {
+            s_av[wave] = v;
+            s_ai[wave] = i;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w = 1; w < 4; ++w) argmax_merge(v, i, s_av[w], s_ai[w]);
+            p.am[blockIdx.x] = ArgmaxPart{v, i};
         }
     }
 }
@@ -1097,6 +1120,31 @@ hipError_t launch_q4_gemv_q8(const Q4Job* jobs, int njobs, const uint32_t* aq, c
                              const int* as, int nb, hipStream_t st) {
     return launch_gemv_q8_any<false>(jobs, njobs, GemvAct{aq, ad, as, nullptr, nullptr, 0.0f},
                                      nb, st);
+}
+
+int q4_gemv_rows_per_part() { return kGemvRows; }
+
+hipError_t launch_q4_gemv_q8_argmax(const Q4Job& job, const uint32_t* aq, const float* ad,
+                                    const int* as, int nb, ArgmaxPart* parts, hipStream_t st) {
+    if (!parts || job.res || nb < 1 || nb > 8 * kChunk) return hipErrorInvalidValue;
+    GemvQ8Params p{};
+    p.m[0] = QMat{job.qs, job.d, job.out, nullptr, job.rows, job.out_stride, q4_scale_stride(nb)};
+    p.tiles[0] = (job.rows + kGemvRows - 1) / kGemvRows;
+    p.nmat = 1;
+    p.a = GemvAct{aq, ad, as, nullptr, nullptr, 0.0f};
+    p.nb = nb;
+    p.am = parts;
+    switch ((nb + kChunk - 1) / kChunk) {
+        case 1: return launch_gemv_q8_t<false, 1>(p, p.tiles[0], st);
+        case 2: return launch_gemv_q8_t<false, 2>(p, p.tiles[0], st);
+        case 3: return launch_gemv_q8_t<false, 3>(p, p.tiles[0], st);
+        case 4: return launch_gemv_q8_t<false, 4>(p, p.tiles[0], st);
+        case 5: return launch_gemv_q8_t<false, 5>(p, p.tiles[0], st);
+        case 6: return launch_gemv_q8_t<false, 6>(p, p.tiles[0], st);
+        case 7: return launch_gemv_q8_t<false, 7>(p, p.tiles[0], st);
+        case 8: return launch_gemv_q8_t<false, 8>(p, p.tiles[0], st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_q4_gemv_norm(const Q4Job* jobs, int njobs, const float* x, const float* w,

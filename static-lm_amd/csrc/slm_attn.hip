@@ -521,6 +521,7 @@ void slm_attn_destroy(slm_attn_ctx* c) {
     (void)hipFree(c->mdl_tok);
     (void)hipFree(c->mdl_logits);
     (void)hipFree(c->mdl_flags);
+    (void)hipFree(c->mdl_parts);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }

@@ -77,6 +77,8 @@ struct slm_attn_ctx {
     size_t mdl_logits_n = 0;
     int32_t* mdl_flags = nullptr;  // [0] argmax, [1] bad token
     size_t mdl_flags_n = 0;
+    slm::ArgmaxPart* mdl_parts = nullptr;  // the lm_head workgroups' best logits
+    size_t mdl_parts_n = 0;
     // kernel timing
     bool profiling = false;
     struct Pending {

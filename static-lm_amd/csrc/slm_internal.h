@@ -155,7 +155,20 @@ hipError_t launch_embed_rows(const uint8_t* qs, const uint16_t* d, int nb, int v
 // out[i] = sum over b in order of rows[b][i] * inv (embed_tokens' pooling)
 hipError_t launch_mean_pool(const float* rows, int n, int dim, float inv, float* out,
                             hipStream_t st);
-// first index of the maximum of x[0..n) (sample_argmax)
-hipError_t launch_argmax(const float* x, int n, int32_t* out, hipStream_t st);
+// The best (value, index) of a stretch of logits, NaN skipped (index -1: none).
+struct ArgmaxPart {
+    float v;
+    int i;
+};
+// One token's projection (as launch_q4_gemv_q8, one matrix, no residual) that
+// also writes each workgroup's ArgmaxPart of its rows: q4_gemv_rows_per_part()
+// rows per part, ceil(rows / that) parts.
+int q4_gemv_rows_per_part();
+hipError_t launch_q4_gemv_q8_argmax(const Q4Job& job, const uint32_t* aq, const float* ad,
+                                    const int* as, int nb, ArgmaxPart* parts, hipStream_t st);
+// sample_argmax from those parts: out[0] = the first index of the maximum of x
+// (0 when x[0] is NaN or every value is)
+hipError_t launch_argmax_parts(const ArgmaxPart* parts, int n_parts, const float* x, int32_t* out,
+                               hipStream_t st);
 
 }  // namespace slm

@@ -254,7 +254,11 @@ int ensure_model(slm_attn_ctx* c, int rows, int vocab) {
         (rc = ensure_buffer(c, &c->mdl_tok, &c->mdl_tok_n, (size_t)rows, "hipMalloc(tokens)")) ||
         (rc = ensure_buffer(c, &c->mdl_logits, &c->mdl_logits_n, (size_t)vocab,
                             "hipMalloc(logits)")) ||
-        (rc = ensure_buffer(c, &c->mdl_flags, &c->mdl_flags_n, 2, "hipMalloc(flags)")))
+        (rc = ensure_buffer(c, &c->mdl_flags, &c->mdl_flags_n, 2, "hipMalloc(flags)")) ||
+        (rc = ensure_buffer(c, &c->mdl_parts, &c->mdl_parts_n,
+                            (size_t)(vocab + slm::q4_gemv_rows_per_part() - 1) /
+                                slm::q4_gemv_rows_per_part(),
+                            "hipMalloc(argmax parts)")))
         return rc;
     return SLM_OK;
 }
@@ -302,16 +306,21 @@ int head(slm_attn_ctx* c, const slm_model_weights* w, float eps, int row, int vo
         t.done();
         if ((rc = run(c, e, "rmsnorm kernel launch"))) return rc;
     }
+    // lm_head; each workgroup also leaves the best of its rows, so the argmax
+    // (sample_argmax, transformer.rs:654-666) merges thousands of parts, not
+    // the whole vocabulary
+    const int n_parts = (vocab + slm::q4_gemv_rows_per_part() - 1) / slm::q4_gemv_rows_per_part();
     {
         const slm::Q4Job job = q4_job(w->lm_head, lg);
         Timed t(c, SLM_K_GEMM);
-        hipError_t e = slm::launch_q4_gemv_q8(&job, 1, c->q8_q, c->q8_d, c->q8_s, nb, c->stream);
+        hipError_t e = slm::launch_q4_gemv_q8_argmax(job, c->q8_q, c->q8_d, c->q8_s, nb,
+                                                     c->mdl_parts, c->stream);
         t.done();
         if ((rc = run(c, e, "q4 projection kernel launch"))) return rc;
     }
     {
         Timed t(c, SLM_K_ELEM);
-        hipError_t e = slm::launch_argmax(lg, vocab, c->mdl_flags, c->stream);
+        hipError_t e = slm::launch_argmax_parts(c->mdl_parts, n_parts, lg, c->mdl_flags, c->stream);
         t.done();
         if ((rc = run(c, e, "argmax kernel launch"))) return rc;
     }
