@@ -228,10 +228,11 @@ def test_larger_model_prefill_matches_token_by_token():
 
 
 def test_argmax_first_maximum_over_a_large_vocabulary():
-    """sample_argmax (transformer.rs:654-666) over 70001 logits, several rounds
-    of the argmax kernel's batched loads: the token is the first index of the
-    maximum of the logits the device returns, also when the maximal lm_head
-    row is copied to a higher index and to a lower one (exact ties)."""
+    """sample_argmax (transformer.rs:654-666) over 70001 logits (4376 lm_head
+    workgroup parts): the token is the first index of the maximum of the
+    logits the device returns, also when the maximal lm_head row is copied to
+    a higher index and to a lower one (exact ties); NaN logits never win,
+    except a NaN at index 0, which gives token 0."""
     cfg, w = ref_model()
     vocab = 70001
     nbytes = cfg.dim // 32 * 18
@@ -265,3 +266,16 @@ def test_argmax_first_maximum_over_a_large_vocabulary():
         dup[lo] = head[m]
         nxt, lg = run(dup)
         assert lg[lo] == lg[m] and nxt == lo
+    # NaN logits (rows whose block scales are f16 NaN): skipped after index 0,
+    # and a NaN at index 0 wins outright (the scan starts from logits[0])
+    nan_rows = head.copy()
+    nan_f16 = np.frombuffer(np.float16(np.nan).tobytes(), np.uint8)
+    for r in (7, vocab - 1, m + 1 if m + 1 < vocab else 5):
+        for b in range(cfg.dim // 32):
+            nan_rows[r, 18 * b:18 * b + 2] = nan_f16
+    nxt, lg = run(nan_rows)
+    assert np.isnan(lg[7]) and nxt == m
+    for b in range(cfg.dim // 32):
+        nan_rows[0, 18 * b:18 * b + 2] = nan_f16
+    nxt, lg = run(nan_rows)
+    assert np.isnan(lg[0]) and nxt == 0
