@@ -109,7 +109,11 @@ int slm_model_prefill_dev(slm_attn_ctx* ctx, const slm_model_weights* w, float r
 /* TransformerModel::generate (transformer.rs:853-899): prefill of the prompt
  * at 0, then greedy decode, writing up to max_out tokens to out_tokens (host)
  * and stopping after `eos` (eos < 0: none) or at max_seq_len.  *n_out is the
- * number written (0 for an empty prompt or max_out == 0). */
+ * number written (0 for an empty prompt or max_out == 0).  The decode steps
+ * are pipelined (each token is read back while the next step runs on the
+ * device), so when generation stops at `eos` one more step has run and been
+ * discarded: the K/V row at the position after the last returned token is
+ * written, which the reference leaves untouched. */
 int slm_model_generate_dev(slm_attn_ctx* ctx, const slm_model_weights* w, float rms_eps,
                            const int32_t* prompt, int32_t n_prompt, int32_t* out_tokens,
                            int32_t max_out, int32_t eos, int32_t* n_out);

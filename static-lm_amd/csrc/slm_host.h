@@ -79,6 +79,8 @@ struct slm_attn_ctx {
     size_t mdl_flags_n = 0;
     slm::ArgmaxPart* mdl_parts = nullptr;  // the lm_head workgroups' best logits
     size_t mdl_parts_n = 0;
+    int32_t* tok_pin = nullptr;            // pinned [2]: generate's tokens, read back
+    hipEvent_t tok_ev[2] = {nullptr, nullptr};  // one step behind the device
     // kernel timing
     bool profiling = false;
     struct Pending {

@@ -6,6 +6,8 @@
 
 #include <string>
 
+#include <algorithm>
+
 #include "slm_host.h"
 
 using namespace slm_host;
@@ -291,9 +293,9 @@ int all_layers(slm_attn_ctx* c, const slm_model_weights* w, float eps, int start
     return SLM_OK;
 }
 
-// Final RMSNorm of model row `row`, lm_head, argmax; *next on the host.
-int head(slm_attn_ctx* c, const slm_model_weights* w, float eps, int row, int vocab,
-         float* logits, int32_t* next) {
+// Final RMSNorm of model row `row`, lm_head, argmax into mdl_flags[0].
+int head_launch(slm_attn_ctx* c, const slm_model_weights* w, float eps, int row, int vocab,
+                float* logits) {
     const slm::Shape& s = c->shape;
     const int nb = s.dim / 32;
     float* lg = logits ? logits : c->mdl_logits;
@@ -324,11 +326,50 @@ int head(slm_attn_ctx* c, const slm_model_weights* w, float eps, int row, int vo
         t.done();
         if ((rc = run(c, e, "argmax kernel launch"))) return rc;
     }
+    return SLM_OK;
+}
+
+// The same, then *next on the host.
+int head(slm_attn_ctx* c, const slm_model_weights* w, float eps, int row, int vocab,
+         float* logits, int32_t* next) {
+    int rc;
+    if ((rc = head_launch(c, w, eps, row, vocab, logits))) return rc;
     int32_t h[2] = {0, 0};
     SLM_HIP(c, hipMemcpyAsync(h, c->mdl_flags, sizeof h, hipMemcpyDeviceToHost, c->stream));
     SLM_HIP(c, hipStreamSynchronize(c->stream));
     if (h[1]) return fail(c, SLM_ERR_TOKEN, "token_id out of vocabulary bounds");
     *next = h[0];
+    return SLM_OK;
+}
+
+// One decode step of generate on the device alone: the token is the previous
+// step's argmax (mdl_flags[0], always in the vocabulary), the new one goes to
+// mdl_flags[0] and, asynchronously, to the pinned slot tok_pin[slot], with
+// tok_ev[slot] recorded after it.
+int decode_step(slm_attn_ctx* c, const slm_model_weights* w, float eps, int pos, int vocab,
+                int slot) {
+    int rc;
+    {
+        Timed t(c, SLM_K_ELEM);
+        hipError_t e = slm::launch_embed_rows(w->token_embd->qs, w->token_embd->d,
+                                              c->shape.dim / 32, vocab, c->mdl_flags, 1,
+                                              c->mdl_x, c->mdl_flags + 1, c->stream);
+        t.done();
+        if ((rc = launch_status(c, e, "embedding kernel launch"))) return rc;
+    }
+    if ((rc = all_layers(c, w, eps, pos, 1)) || (rc = head_launch(c, w, eps, 0, vocab, nullptr)))
+        return rc;
+    SLM_HIP(c, hipMemcpyAsync(c->tok_pin + slot, c->mdl_flags, sizeof(int32_t),
+                              hipMemcpyDeviceToHost, c->stream));
+    SLM_HIP(c, hipEventRecord(c->tok_ev[slot], c->stream));
+    return SLM_OK;
+}
+
+int ensure_token_readback(slm_attn_ctx* c) {
+    if (!c->tok_pin) SLM_HIP(c, hipHostMalloc(reinterpret_cast<void**>(&c->tok_pin),
+                                              2 * sizeof(int32_t), hipHostMallocDefault));
+    for (hipEvent_t& e : c->tok_ev)
+        if (!e) SLM_HIP(c, hipEventCreateWithFlags(&e, hipEventDisableTiming));
     return SLM_OK;
 }
 
@@ -385,14 +426,26 @@ int slm_model_generate_dev(slm_attn_ctx* c, const slm_model_weights* w, float rm
         *n_out = generated;
         return SLM_OK;
     }
-    for (int pos = n_prompt; generated < max_out && pos < c->cfg.max_seq_len; ++pos) {
-        if ((rc = model_prefill(c, w, rms_eps, &next, 1, pos, nullptr, &next))) {
+    // Greedy decode (:867-897), pipelined: step k's token is read on the host
+    // while step k + 1 already runs, so the device never waits for the host;
+    // a step launched after the EOS token is drained and its token dropped
+    // (its K/V row, one past the returned sequence, is written).
+    const int steps = std::min(max_out - 1, c->cfg.max_seq_len - n_prompt);
+    int vocab = 0;
+    if ((rc = check_model(c, w, &vocab)) || (rc = ensure_token_readback(c))) return rc;
+    for (int k = 0; k <= steps; ++k) {
+        if (k < steps && (rc = decode_step(c, w, rms_eps, n_prompt + k, vocab, k & 1))) {
+            (void)hipStreamSynchronize(c->stream);
             *n_out = generated;
             return rc;
         }
+        if (k == 0) continue;
+        SLM_HIP(c, hipEventSynchronize(c->tok_ev[(k - 1) & 1]));
+        next = c->tok_pin[(k - 1) & 1];
         out_tokens[generated++] = next;
         if (eos >= 0 && next == eos) break;
     }
+    SLM_HIP(c, hipStreamSynchronize(c->stream));
     *n_out = generated;
     return SLM_OK;
 }
