@@ -35,11 +35,17 @@ __device__ __forceinline__ float2 rope_pair_exact(float2 x, float c, float s) {
     return r;
 }
 
-// Two consecutive pairs (x,y), (z,w) at table columns j, j+1, bit-exact.
-__device__ __forceinline__ float4 rope4_exact(float4 x, const float* c, const float* s) {
-    const float2 a = rope_pair_exact(make_float2(x.x, x.y), c[0], s[0]);
-    const float2 b = rope_pair_exact(make_float2(x.z, x.w), c[1], s[1]);
+// Two consecutive pairs (x,y), (z,w) with table entries (c.x, s.x), (c.y,
+// s.y), bit-exact.
+__device__ __forceinline__ float4 rope4_exact(float4 x, float2 c, float2 s) {
+    const float2 a = rope_pair_exact(make_float2(x.x, x.y), c.x, s.x);
+    const float2 b = rope_pair_exact(make_float2(x.z, x.w), c.y, s.y);
     return make_float4(a.x, a.y, b.x, b.y);
+}
+
+// The same with the entries read at table columns j, j+1.
+__device__ __forceinline__ float4 rope4_exact(float4 x, const float* c, const float* s) {
+    return rope4_exact(x, make_float2(c[0], c[1]), make_float2(s[0], s[1]));
 }
 
 template <int CTRL>

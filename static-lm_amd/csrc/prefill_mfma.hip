@@ -109,17 +109,39 @@ prefill_mfma_kernel(PrefillParams p) {
     const int wave_last_pos = p.start + q0 + wave_rows - 1;
 
     // Q fragments: row q0 + qt*16 + lr, dims lg*DPL .. +DPL, rotated, scaled.
-    float qf[NQT][DPL];
+    // All q and table loads are issued before the first use (a load inside
+    // the rotate branch would wait for every earlier load, once per float4).
+    const bool rot = p.cos_t != nullptr;
+    float4 qx[NQT][DPL / 4];
+    float2 qc[NQT][DPL / 4], qsn[NQT][DPL / 4];
+    bool qok[NQT];
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
         const int row = q0 + qt * 16 + lr;
-        const bool ok = row < p.n;
-        const float* src = p.q + (long)(ok ? row : 0) * p.dim + head * HD + lg * DPL;
-        const long tr = (long)(p.start + (ok ? row : 0)) * p.half + (lg * DPL >> 1);
+        qok[qt] = row < p.n;
+        const float* src = p.q + (long)(qok[qt] ? row : 0) * p.dim + head * HD + lg * DPL;
+#pragma unroll
+        for (int c = 0; c < DPL / 4; ++c) qx[qt][c] = ld4(src + 4 * c);  // zeroed below if !ok
+    }
+    if (rot) {
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+            const int row = min(q0 + qt * 16 + lr, p.n - 1);
+            const long tr = (long)(p.start + row) * p.half + (lg * DPL >> 1);
+#pragma unroll
+            for (int c = 0; c < DPL / 4; ++c) {
+                qc[qt][c] = *reinterpret_cast<const float2*>(p.cos_t + tr + 2 * c);
+                qsn[qt][c] = *reinterpret_cast<const float2*>(p.sin_t + tr + 2 * c);
+            }
+        }
+    }
+    float qf[NQT][DPL];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
 #pragma unroll
         for (int c = 0; c < DPL / 4; ++c) {
-            float4 x = ok ? ld4(src + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (p.cos_t != nullptr) x = rope4_exact(x, p.cos_t + tr + 2 * c, p.sin_t + tr + 2 * c);
+            float4 x = qok[qt] ? qx[qt][c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (rot) x = rope4_exact(x, qc[qt][c], qsn[qt][c]);
             qf[qt][4 * c + 0] = x.x * p.scale_log2;
             qf[qt][4 * c + 1] = x.y * p.scale_log2;
             qf[qt][4 * c + 2] = x.z * p.scale_log2;
