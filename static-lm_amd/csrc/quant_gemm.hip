@@ -906,6 +906,45 @@ __global__ __launch_bounds__(64 * WRW * WTW) void gemm_q4_mfma_kernel(GemmParams
         if (sg + 1 < n_stages) SLM_GEMM_STORE_STAGE(st[(sg + 1) & 1]);
     }
 
+    // Rows r0..r0+3 of token t (r0 a multiple of 4) are contiguous in out and
+    // res: with whole 4-row groups and 16-byte aligned rows they move as one
+    // 128-bit access, and every residual load (at a clamped, in-bounds
+    // address) is issued before the first add, so the epilogue costs one
+    // memory round trip rather than one per element.
+    const bool vec = (M.rows & 3) == 0 && (M.out_stride & 3) == 0 &&
+                     ((reinterpret_cast<uintptr_t>(M.out) | reinterpret_cast<uintptr_t>(M.res)) &
+                      15) == 0;
+    if (vec) {
+        float4 rv[2][NTS];
+        if (M.res) {
+#pragma unroll
+            for (int rs2 = 0; rs2 < 2; ++rs2)
+#pragma unroll
+                for (int ts = 0; ts < NTS; ++ts) {
+                    const int t = min(wt0 + qt + 16 * ts + lr, p.batch - 1);
+                    const int r0 = min(wr0 + qr + 16 * rs2 + 4 * g, M.rows - 4);
+                    rv[rs2][ts] = ld4(M.res + (long)t * M.out_stride + r0);
+                }
+        }
+#pragma unroll
+        for (int rs2 = 0; rs2 < 2; ++rs2)
+#pragma unroll
+            for (int ts = 0; ts < NTS; ++ts) {
+                const int t = wt0 + qt + 16 * ts + lr;
+                const int r0 = wr0 + qr + 16 * rs2 + 4 * g;
+                if (t >= p.batch || r0 >= M.rows) continue;
+                float4 y = make_float4(acc[rs2][ts][0], acc[rs2][ts][1], acc[rs2][ts][2],
+                                       acc[rs2][ts][3]);
+                if (M.res) {
+                    y.x = rv[rs2][ts].x + y.x;
+                    y.y = rv[rs2][ts].y + y.y;
+                    y.z = rv[rs2][ts].z + y.z;
+                    y.w = rv[rs2][ts].w + y.w;
+                }
+                *reinterpret_cast<float4*>(M.out + (long)t * M.out_stride + r0) = y;
+            }
+        return;
+    }
 #pragma unroll
     for (int rs2 = 0; rs2 < 2; ++rs2)
 #pragma unroll

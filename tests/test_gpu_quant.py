@@ -213,6 +213,8 @@ RESIDUAL_CASES = [
     (576, 576, 4),        # GEMV batch 4
     (288, 768, 7),        # MFMA GEMM, ragged row and token tiles
     (4096, 14336, 65),    # MFMA GEMM, two token tiles
+    (4096, 4096, 130),    # MFMA GEMM with 128-token tiles, ragged last tile
+    (90, 256, 9),         # rows not a multiple of 4: the per-element epilogue
 ]
 
 
