@@ -188,32 +188,79 @@ __device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
 // Merges the online-softmax states of the lane groups of a wave (lanes with
 // equal index inside their group hold equal head dims); afterwards every
 // lane holds the wave's state for its dims.
-template <int LPG, int NV, int GB>
-__device__ __forceinline__ void merge_lane_groups(float (&m)[GB], float (&l)[GB],
-                                                  float4 (&o)[GB][NV]) {
-#pragma unroll
-    for (int off = LPG; off < 64; off <<= 1) {
+// The values of lanes l and l ^ OFF, in an order that depends on the lane
+// alone (the same for every call): gfx950's VALU lane swaps for OFF 16 and
+// 32, a DPP row rotation for 8, a shuffle below that.
+template <int OFF>
+__device__ __forceinline__ void lane_pair(float x, float& a, float& b) {
+    if constexpr (OFF == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                        false, false);
+        a = __uint_as_float(r[0]);
+        b = __uint_as_float(r[1]);
+    } else if constexpr (OFF == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                        false, false);
+        a = __uint_as_float(r[0]);
+        b = __uint_as_float(r[1]);
+    } else if constexpr (OFF == 8) {
+        a = x;
+        b = dpp<0x128>(x);  // row_ror:8 — lane l ^ 8 within its 16-lane row
+    } else {
+        a = x;
+        b = __shfl_xor(x, OFF);
+    }
+}
+
+// a*wa + b*wb with both products rounded before the add, so the two lanes of
+// a pair (which see the operands in opposite orders) get the same bits.
+__device__ __forceinline__ float pair_sum(float a, float wa, float b, float wb) {
+#pragma clang fp contract(off)
+    return a * wa + b * wb;
+}
+
+// Merges the online-softmax states of lane groups OFF apart, then the next
+// level up to the whole wave.
+template <int OFF, int NV, int GB>
+__device__ __forceinline__ void merge_lane_round(float (&m)[GB], float (&l)[GB],
+                                                 float4 (&o)[GB][NV]) {
+    if constexpr (OFF < 64) {
 #pragma unroll
         for (int i = 0; i < GB; ++i) {
-            const float mo = __shfl_xor(m[i], off);
-            const float lo = __shfl_xor(l[i], off);
-            const float mn = fmaxf(m[i], mo);
+            float ma, mb, la, lb;
+            lane_pair<OFF>(m[i], ma, mb);
+            lane_pair<OFF>(l[i], la, lb);
+            const float mn = fmaxf(ma, mb);
             const float mu = (mn == -INFINITY) ? 0.0f : mn;
-            const float wa = fast_exp2(m[i] - mu);
-            const float wb = fast_exp2(mo - mu);
-            l[i] = l[i] * wa + lo * wb;
+            const float wa = fast_exp2(ma - mu);
+            const float wb = fast_exp2(mb - mu);
+            l[i] = pair_sum(la, wa, lb, wb);
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
                 float4 x = o[i][v];
-                x.x = x.x * wa + __shfl_xor(x.x, off) * wb;
-                x.y = x.y * wa + __shfl_xor(x.y, off) * wb;
-                x.z = x.z * wa + __shfl_xor(x.z, off) * wb;
-                x.w = x.w * wa + __shfl_xor(x.w, off) * wb;
+                float xa, xb;
+                lane_pair<OFF>(x.x, xa, xb);
+                x.x = pair_sum(xa, wa, xb, wb);
+                lane_pair<OFF>(x.y, xa, xb);
+                x.y = pair_sum(xa, wa, xb, wb);
+                lane_pair<OFF>(x.z, xa, xb);
+                x.z = pair_sum(xa, wa, xb, wb);
+                lane_pair<OFF>(x.w, xa, xb);
+                x.w = pair_sum(xa, wa, xb, wb);
                 o[i][v] = x;
             }
             m[i] = mn;
         }
+        merge_lane_round<2 * OFF, NV, GB>(m, l, o);
     }
+}
+
+// Merges the states of the 64 / LPG lane groups of a wave; every lane ends
+// with the wave's state.
+template <int LPG, int NV, int GB>
+__device__ __forceinline__ void merge_lane_groups(float (&m)[GB], float (&l)[GB],
+                                                  float4 (&o)[GB][NV]) {
+    merge_lane_round<LPG, NV, GB>(m, l, o);
 }
 
 // Query heads that share one loaded K/V segment in a workgroup.

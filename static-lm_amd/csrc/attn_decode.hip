@@ -475,6 +475,10 @@ hipError_t launch_decode_combine(const Shape& s, const DecodeArgs& a, hipStream_
 hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st) {
     const DecodeParams dp = decode_params(s, a);
     if (a.n_splits < 1 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
+    // the appended k row is rotated with the tables (the kernel reads them
+    // whenever it appends)
+    if (a.k_new != nullptr && (a.cos_t == nullptr || a.sin_t == nullptr || a.v_new == nullptr))
+        return hipErrorInvalidValue;
     switch (s.head_dim) {
         case 16: return launch_hd<16>(s, dp, st);
         case 32: return launch_hd<32>(s, dp, st);
