@@ -94,16 +94,24 @@ __device__ __forceinline__ float rows_sum(float x) {
 // satisfies the invariant, so the normalised result is unchanged.
 constexpr float kLazyRescale = 8.0f;
 
+// Max / sum over the wave, every lane getting the result: DPP row rotations
+// by 8, 4, 2 and 1 fold each 16-lane row (lane l then holds the whole row's
+// value), the lane swaps fold the four rows.  All VALU, no LDS round trips.
+// The sum's association differs from lane to lane.
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-    return x;
+    x = fmaxf(x, dpp<0x128>(x));  // row_ror:8
+    x = fmaxf(x, dpp<0x124>(x));  // row_ror:4
+    x = fmaxf(x, dpp<0x122>(x));  // row_ror:2
+    x = fmaxf(x, dpp<0x121>(x));  // row_ror:1
+    return rows_max(x);
 }
 
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-    return x;
+    x += dpp<0x128>(x);
+    x += dpp<0x124>(x);
+    x += dpp<0x122>(x);
+    x += dpp<0x121>(x);
+    return rows_sum(x);
 }
 
 // Lanes per position group for each compiled head_dim: every lane holds
