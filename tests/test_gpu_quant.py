@@ -77,9 +77,13 @@ GEMM_CASES = [
     (288, 288, 17),     # ragged row and token tiles
     (4096, 4096, 64),
     (320, 8192, 100),
-    (288, 288, 128),    # the 128 x 128 workgroups from 128 tokens: ragged row tile
+    (288, 288, 128),    # ragged row tile
     (1024, 4096, 300),  # ragged token tile
-    (96, 16384, 130),   # nb 512 with the wide workgroups
+    (96, 16384, 130),   # nb 512
+    # enough 128 x 128 tiles to fill 256 CUs, where the launcher picks them
+    # over 64 x 64 (Llama-3-8B Q/K/V and gate/up at 4096 tokens do too)
+    (8192, 256, 2048),
+    (16380, 64, 1000),  # ragged row and token tiles of the 128 x 128 workgroups
 ]
 
 
@@ -213,7 +217,8 @@ RESIDUAL_CASES = [
     (576, 576, 4),        # GEMV batch 4
     (288, 768, 7),        # MFMA GEMM, ragged row and token tiles
     (4096, 14336, 65),    # MFMA GEMM, two token tiles
-    (4096, 4096, 130),    # MFMA GEMM with 128-token tiles, ragged last tile
+    (4096, 4096, 130),    # MFMA GEMM, ragged last token tile
+    (16380, 64, 1000),    # 128 x 128 workgroups (on 256 CUs), ragged row and token tiles
     (90, 256, 9),         # rows not a multiple of 4: the per-element epilogue
 ]
 
