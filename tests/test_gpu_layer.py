@@ -232,6 +232,43 @@ def test_layer_forward_equals_composed_entry_points(dim, hidden, heads, kvh, msl
         blk.close()
 
 
+# Decode positions where the split-K merge runs (more than 8 tiles of cache
+# rows); the layer tests above decode within one split.
+SPLIT_DECODE_SHAPES = [
+    # dim, hidden, heads, kv_heads, msl, prefill rows (tiles of 32 rows for hd 128, 64 for hd 64)
+    (1024, 512, 8, 2, 320, 290),
+    (576, 1536, 9, 3, 640, 580),
+]
+
+
+@pytest.mark.parametrize("dim,hidden,heads,kvh,msl,pre", SPLIT_DECODE_SHAPES)
+def test_layer_decode_with_split_merge_equals_composed(dim, hidden, heads, kvh, msl, pre):
+    kvd = dim // heads * kvh
+    eps = 1e-5
+    log(f"split decode block dim {dim} heads {heads}/{kvh} after {pre} rows")
+    blk = Block(51, dim, kvd, hidden)
+    calls = [(0, pre), (pre, 1), (pre + 1, 1), (pre + 2, 3), (pre + 5, 1)]
+    try:
+        with P.AttentionContext(dim, heads, kvh, msl, 1, 1e4) as a, \
+                P.AttentionContext(dim, heads, kvh, msl, 1, 1e4) as b:
+            assert a.decode_splits(pre + 1)[0] > 1
+            x0 = gen([52, dim], (msl, dim))
+            xa = dev(x0)
+            xb_ = dev(x0)
+            for start, n in calls:
+                log(f"  start {start} n {n}")
+                rows = xa[start:start + n]
+                a.layer_forward_dev(0, start, n, blk.dev, eps, rows.data_ptr())
+                out = composed_step(b, blk, 0, start, n, xb_[start:start + n], eps)
+                xb_[start:start + n].copy_(out)
+                torch.cuda.synchronize()
+            a.sync()
+            b.sync()
+            assert_bitwise(xa.cpu().numpy(), xb_.cpu().numpy(), "residual stream")
+    finally:
+        blk.close()
+
+
 @pytest.mark.parametrize("dim,hidden,heads,kvh,msl", BLOCK_SHAPES[:2])
 def test_layer_forward_against_oracle(dim, hidden, heads, kvh, msl):
     """Each call against the oracle's block from the device's state before it
