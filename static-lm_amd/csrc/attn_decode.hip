@@ -31,6 +31,7 @@
 // registers with the reference's f32 arithmetic (no FMA contraction), stores
 // K[p] and V[p] (bit-exact with the reference), and seeds its state with
 // them.  No other workgroup reads row p.
+#include <hip/hip_ext.h>
 #include <math.h>
 
 #include "attn_common.h"
@@ -369,10 +370,15 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p
 }
 
 template <int HD, int GB>
-hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st) {
+hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st, hipEvent_t ev0,
+                    hipEvent_t ev1) {
     const int groups = s.num_kv_heads * (s.kv_mul / GB);
-    hipLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups),
-                       dim3(64 * DecodeCfg<HD>::NW), 0, st, dp);
+    if (ev0 != nullptr && ev1 != nullptr)
+        hipExtLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups),
+                              dim3(64 * DecodeCfg<HD>::NW), 0, st, ev0, ev1, 0, dp);
+    else
+        hipLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups),
+                           dim3(64 * DecodeCfg<HD>::NW), 0, st, dp);
     return hipGetLastError();
 }
 
@@ -385,12 +391,13 @@ hipError_t launch_combine_t(const Shape& s, const DecodeParams& dp, hipStream_t 
 }
 
 template <int HD>
-hipError_t launch_hd(const Shape& s, const DecodeParams& dp, hipStream_t st) {
+hipError_t launch_hd(const Shape& s, const DecodeParams& dp, hipStream_t st, hipEvent_t ev0,
+                     hipEvent_t ev1) {
     switch (pick_gb(s.kv_mul)) {
-        case 4: return launch_t<HD, 4>(s, dp, st);
-        case 3: return launch_t<HD, 3>(s, dp, st);
-        case 2: return launch_t<HD, 2>(s, dp, st);
-        default: return launch_t<HD, 1>(s, dp, st);
+        case 4: return launch_t<HD, 4>(s, dp, st, ev0, ev1);
+        case 3: return launch_t<HD, 3>(s, dp, st, ev0, ev1);
+        case 2: return launch_t<HD, 2>(s, dp, st, ev0, ev1);
+        default: return launch_t<HD, 1>(s, dp, st, ev0, ev1);
     }
 }
 
@@ -480,13 +487,13 @@ hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st) {
     if (a.k_new != nullptr && (a.cos_t == nullptr || a.sin_t == nullptr || a.v_new == nullptr))
         return hipErrorInvalidValue;
     switch (s.head_dim) {
-        case 16: return launch_hd<16>(s, dp, st);
-        case 32: return launch_hd<32>(s, dp, st);
-        case 48: return launch_hd<48>(s, dp, st);
-        case 64: return launch_hd<64>(s, dp, st);
-        case 96: return launch_hd<96>(s, dp, st);
-        case 128: return launch_hd<128>(s, dp, st);
-        case 256: return launch_hd<256>(s, dp, st);
+        case 16: return launch_hd<16>(s, dp, st, a.ev_start, a.ev_stop);
+        case 32: return launch_hd<32>(s, dp, st, a.ev_start, a.ev_stop);
+        case 48: return launch_hd<48>(s, dp, st, a.ev_start, a.ev_stop);
+        case 64: return launch_hd<64>(s, dp, st, a.ev_start, a.ev_stop);
+        case 96: return launch_hd<96>(s, dp, st, a.ev_start, a.ev_stop);
+        case 128: return launch_hd<128>(s, dp, st, a.ev_start, a.ev_stop);
+        case 256: return launch_hd<256>(s, dp, st, a.ev_start, a.ev_stop);
         default: return hipErrorInvalidValue;
     }
 }

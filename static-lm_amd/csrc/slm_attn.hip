@@ -207,9 +207,12 @@ int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* 
                       pos,
                       ns};
     {
-        Timed t(c, SLM_K_DECODE);
+        // the launch stamps the events at the kernel's own start and end
+        Timed t(c, SLM_K_DECODE, /*in_launch=*/true);
+        a.ev_start = t.b;
+        a.ev_stop = t.e;
         hipError_t e = slm::launch_decode(s, a, c->stream);
-        t.done();
+        t.done_in_launch(e == hipSuccess);
         if (e != hipSuccess) return hip_fail(c, e, "decode kernel launch");
     }
     if (ns == 1) return SLM_OK;

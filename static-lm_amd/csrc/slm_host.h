@@ -115,11 +115,25 @@ struct Timed {
     int kind;
     hipEvent_t b = nullptr;
     hipEvent_t e = nullptr;
-    Timed(slm_attn_ctx* ctx, int k) : c(ctx), kind(k) {
+    // in_launch: the launch itself records b and e (hipExtLaunchKernelGGL
+    // stamps them at the kernel's start and end, as a kernel trace does);
+    // otherwise b is recorded here and e by done()
+    Timed(slm_attn_ctx* ctx, int k, bool in_launch = false) : c(ctx), kind(k) {
         if (!c->profiling) return;
         b = take_event(c);
         e = take_event(c);
+        if (in_launch) return;
         if (b && e && hipEventRecord(b, c->stream) != hipSuccess) drop();
+    }
+    // after a launch that recorded b and e itself
+    void done_in_launch(bool launched) {
+        if (!b || !e) return;
+        if (!launched) {
+            drop();
+            return;
+        }
+        c->pending.push_back({kind, b, e});
+        b = e = nullptr;
     }
     void done() {
         if (!b || !e) return;

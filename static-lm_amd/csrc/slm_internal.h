@@ -48,6 +48,9 @@ struct DecodeArgs {
     float* part_ml;      // [n_splits][num_heads][2]
     int pos;
     int n_splits;
+    // when set, the decode kernel's launch records these at its start and end
+    hipEvent_t ev_start = nullptr;
+    hipEvent_t ev_stop = nullptr;
 };
 // Split count and tile length (positions) at seq_len: split s of n reads
 // tiles s, s+n, s+2n, ...  A pure function of seq_len, the shape and the CU
