@@ -383,10 +383,15 @@ hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st, hipE
 }
 
 template <int HD>
-hipError_t launch_combine_t(const Shape& s, const DecodeParams& dp, hipStream_t st) {
+hipError_t launch_combine_t(const Shape& s, const DecodeParams& dp, hipStream_t st,
+                            hipEvent_t ev0, hipEvent_t ev1) {
     constexpr int DW = combine_width<HD>();
-    hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads, HD / DW), dim3(kThreads), 0,
-                       st, dp);
+    if (ev0 != nullptr && ev1 != nullptr)
+        hipExtLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads, HD / DW),
+                              dim3(kThreads), 0, st, ev0, ev1, 0, dp);
+    else
+        hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads, HD / DW),
+                           dim3(kThreads), 0, st, dp);
     return hipGetLastError();
 }
 
@@ -468,13 +473,13 @@ hipError_t launch_decode_combine(const Shape& s, const DecodeArgs& a, hipStream_
     const DecodeParams dp = decode_params(s, a);
     if (a.n_splits < 2 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
     switch (s.head_dim) {
-        case 16: return launch_combine_t<16>(s, dp, st);
-        case 32: return launch_combine_t<32>(s, dp, st);
-        case 48: return launch_combine_t<48>(s, dp, st);
-        case 64: return launch_combine_t<64>(s, dp, st);
-        case 96: return launch_combine_t<96>(s, dp, st);
-        case 128: return launch_combine_t<128>(s, dp, st);
-        case 256: return launch_combine_t<256>(s, dp, st);
+        case 16: return launch_combine_t<16>(s, dp, st, a.ev_start, a.ev_stop);
+        case 32: return launch_combine_t<32>(s, dp, st, a.ev_start, a.ev_stop);
+        case 48: return launch_combine_t<48>(s, dp, st, a.ev_start, a.ev_stop);
+        case 64: return launch_combine_t<64>(s, dp, st, a.ev_start, a.ev_stop);
+        case 96: return launch_combine_t<96>(s, dp, st, a.ev_start, a.ev_stop);
+        case 128: return launch_combine_t<128>(s, dp, st, a.ev_start, a.ev_stop);
+        case 256: return launch_combine_t<256>(s, dp, st, a.ev_start, a.ev_stop);
         default: return hipErrorInvalidValue;
     }
 }

@@ -216,9 +216,11 @@ int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* 
         if (e != hipSuccess) return hip_fail(c, e, "decode kernel launch");
     }
     if (ns == 1) return SLM_OK;
-    Timed t(c, SLM_K_COMBINE);
+    Timed t(c, SLM_K_COMBINE, /*in_launch=*/true);
+    a.ev_start = t.b;
+    a.ev_stop = t.e;
     hipError_t e = slm::launch_decode_combine(s, a, c->stream);
-    t.done();
+    t.done_in_launch(e == hipSuccess);
     return launch_status(c, e, "decode combine kernel launch");
 }
 

@@ -48,7 +48,8 @@ struct DecodeArgs {
     float* part_ml;      // [n_splits][num_heads][2]
     int pos;
     int n_splits;
-    // when set, the decode kernel's launch records these at its start and end
+    // when set, the launch (decode or merge) records these at the kernel's
+    // start and end
     hipEvent_t ev_start = nullptr;
     hipEvent_t ev_stop = nullptr;
 };
