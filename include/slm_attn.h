@@ -172,9 +172,12 @@ float* slm_kv_device_ptr(const slm_attn_ctx* ctx);
 int slm_rope_tables_read(slm_attn_ctx* ctx, float* cos_out, float* sin_out);
 
 /* ---- kernel timing -------------------------------------------------------
- * While enabled, every launch is bracketed by HIP events on the context
+ * While enabled, every launch is timed with HIP events on the context
  * stream, and slm_attn_profile_read() returns, per kernel kind, the number
  * of launches and their summed duration in ms (it synchronizes the stream).
+ * The decode and merge launches stamp their events at the kernel's own start
+ * and end (as a kernel trace measures); other kinds are bracketed by events
+ * recorded around the launch, which adds its dispatch (~2 us).
  * Reading resets the counters. */
 enum {
     SLM_K_APPEND = 0,  /* rope(k) + KV append of a prefill batch */
