@@ -50,7 +50,9 @@ extern "C" {
 #define SLM_ERR_BATCH (-3)
 /* layer index outside 0..num_layers (the layer-count assert, transformer.rs:761-766). */
 #define SLM_ERR_LAYER (-4)
-/* out overlaps q, k, v or the KV region (attention_slices, arena.rs:272-280). */
+/* out overlaps q, k, v or the KV region (attention_slices, arena.rs:272-280),
+ * or an input of an appending call (decode, prefill, KV append) overlaps the
+ * KV region: k and v are staging rows, not cache rows. */
 #define SLM_ERR_ALIAS (-5)
 /* NULL pointer, which not in {0,1}, or a row range outside the cache
  * (ArenaSlice::subslice bounds, arena.rs:27-36). */
@@ -165,7 +167,10 @@ int slm_kv_write_dev(slm_attn_ctx* ctx, int32_t layer, int32_t which,
 size_t slm_kv_offset(const slm_attn_ctx* ctx, int32_t layer, int32_t which,
                      int32_t pos);
 
-/* Device address of the KV region base (for zero-copy producers). */
+/* Device address of the KV region base, for producers that write final
+ * (already rotated) rows in place and then call slm_attn_attend_dev /
+ * slm_attn_attend_batch_dev.  The appending calls (decode, prefill, KV
+ * append) refuse inputs that point into this region (SLM_ERR_ALIAS). */
 float* slm_kv_device_ptr(const slm_attn_ctx* ctx);
 
 /* Copy the device RoPE tables [max_seq_len][head_dim/2] back to the host. */

@@ -129,7 +129,11 @@ typedef struct slm_model slm_model;
 /* GgufFile::model_weights (loader.rs:523-552) for num_layers layers, uploaded
  * to `device`: token_embd.weight (Q4_0, vocab = dims[1]), blk.{l}.attn_norm /
  * attn_q / attn_k / attn_v / attn_output / ffn_norm / ffn_gate / ffn_up /
- * ffn_down, output_norm.weight, output.weight (token_embd when absent). */
+ * ffn_down, output_norm.weight, output.weight (token_embd when absent).
+ * Every tensor is checked before anything is uploaded: a missing one or one
+ * of the wrong type gives its GgufError code, and a norm vector whose length
+ * is not the model dimension (token_embd's dims[0]) gives SLM_ERR_SHAPE (the
+ * reference's RMSNorm asserts weights.len() == dst.len, engine.rs:199). */
 int slm_model_load_gguf(const slm_gguf* g, int32_t device, int32_t num_layers,
                         slm_model** out);
 void slm_model_destroy(slm_model* m);

@@ -68,8 +68,8 @@ typedef struct slm_layer_weights {
  * residual -> RMSNorm -> gate, up -> SwiGLU -> down + residual, with the
  * reference's arithmetic in every step (projections bit-identical to the
  * scalar dot, attention within 1e-4 / 1e-3).  rms_eps is
- * TransformerConfig::rms_eps; hidden_dim must be a multiple of 32 and at most
- * 16384. */
+ * TransformerConfig::rms_eps; dim at most 16384 and hidden_dim a multiple of
+ * 32 and at most 16384 (SLM_ERR_SHAPE otherwise). */
 int slm_layer_forward_dev(slm_attn_ctx* ctx, int32_t layer, int32_t start, int32_t n,
                           const slm_layer_weights* w, float rms_eps, float* x);
 

@@ -171,6 +171,21 @@ int check_out_alias(slm_attn_ctx* c, const float* out, size_t out_floats,
     return SLM_OK;
 }
 
+// Inputs of an entry point that appends to the cache must not overlap the
+// KV region: the kernels write row pos (rows start..start+n-1) while other
+// workgroups read the inputs, so a k taken from the cache row it is appended
+// to would be read after its rotation by some workgroups and before it by
+// others.  (The reference's GEMV writes k into the cache row and rotates it
+// there, transformer.rs:416-428; here k and v come from staging buffers.)
+int check_in_not_kv(slm_attn_ctx* c,
+                    std::initializer_list<std::pair<const float*, size_t>> ins) {
+    for (const auto& in : ins)
+        if (in.first && overlaps(in.first, in.second * 4, c->kv, c->kv_floats * 4))
+            return fail(c, SLM_ERR_ALIAS,
+                        "q, k and v of an appending call must not overlap the KV cache");
+    return SLM_OK;
+}
+
 int launch_status(slm_attn_ctx* c, hipError_t e, const char* what) {
     if (e != hipSuccess) return hip_fail(c, e, what);
     return SLM_OK;
@@ -557,6 +572,8 @@ int slm_kv_append_dev(slm_attn_ctx* c, int32_t layer, int32_t pos0, int32_t n,
     if ((rc = check_layer(c, layer)) || (rc = check_batch(c, pos0, n)) ||
         (rc = check_dev_ptrs(c, {k, v})))
         return rc;
+    const size_t kn = (size_t)n * c->shape.kv_dim;
+    if ((rc = check_in_not_kv(c, {{k, kn}, {v, kn}}))) return rc;
     return do_append(c, layer, pos0, n, k, v);
 }
 
@@ -609,7 +626,8 @@ int slm_attn_decode_dev(slm_attn_ctx* c, int32_t layer, int32_t pos,
         (rc = check_dev_ptrs(c, {q, k, v, out})) ||
         (rc = check_out_alias(c, out, s.dim,
                               {{q, s.dim}, {k, s.kv_dim}, {v, s.kv_dim}},
-                              true)))
+                              true)) ||
+        (rc = check_in_not_kv(c, {{q, s.dim}, {k, s.kv_dim}, {v, s.kv_dim}})))
         return rc;
     return do_decode(c, layer, pos, q, k, v, out, true);
 }
@@ -624,7 +642,8 @@ int slm_attn_prefill_dev(slm_attn_ctx* c, int32_t layer, int32_t start,
         (rc = check_dev_ptrs(c, {q, k, v, out})))
         return rc;
     const size_t qn = (size_t)n * s.dim, kn = (size_t)n * s.kv_dim;
-    if ((rc = check_out_alias(c, out, qn, {{q, qn}, {k, kn}, {v, kn}}, true)))
+    if ((rc = check_out_alias(c, out, qn, {{q, qn}, {k, kn}, {v, kn}}, true)) ||
+        (rc = check_in_not_kv(c, {{q, qn}, {k, kn}, {v, kn}})))
         return rc;
     if ((rc = do_append(c, layer, start, n, k, v))) return rc;
     return do_attend(c, layer, start, n, q, out, true);

@@ -122,6 +122,10 @@ struct Timed {
         if (!c->profiling) return;
         b = take_event(c);
         e = take_event(c);
+        if (!b || !e) {  // a launch is timed with both events or not at all
+            drop();
+            return;
+        }
         if (in_launch) return;
         if (b && e && hipEventRecord(b, c->stream) != hipSuccess) drop();
     }

@@ -52,6 +52,9 @@ int norm_common(slm_attn_ctx* c, const float* x, const float* w, int rows, int n
 int check_weights(slm_attn_ctx* c, const slm_layer_weights* w, int* hidden) {
     const slm::Shape& s = c->shape;
     if (!w) return fail(c, SLM_ERR_ARG, "weights is NULL");
+    // the one-token projections read a whole dim-long row per workgroup
+    if (s.dim > slm::q4_max_cols())
+        return fail(c, SLM_ERR_SHAPE, "dim above 16384 is not compiled for the projections");
     int rc;
     if ((rc = check_matrix(c, w->wq, s.dim, s.dim, "wq")) ||
         (rc = check_matrix(c, w->wk, s.kv_dim, s.dim, "wk")) ||
@@ -238,6 +241,8 @@ int check_model(slm_attn_ctx* c, const slm_model_weights* w, int* vocab) {
     if (!w || !w->layers) return fail(c, SLM_ERR_ARG, "weights is NULL");
     if (w->num_layers != c->cfg.num_layers)
         return fail(c, SLM_ERR_CONFIG, "layer count mismatch");  // transformer.rs:762-766
+    if (s.dim > slm::q4_max_cols())
+        return fail(c, SLM_ERR_SHAPE, "dim above 16384 is not compiled for the projections");
     int rc;
     if (!w->token_embd) return fail(c, SLM_ERR_ARG, "token_embd is NULL");
     const int v = w->token_embd->rows;

@@ -42,18 +42,70 @@ int load_q4(slm_model* m, const slm_gguf* g, const std::string& name,
     return SLM_OK;
 }
 
-int load_f32(slm_model* m, const slm_gguf* g, const std::string& name, const float** out) {
+// An f32 vector of exactly `floats` elements: the norm kernels read that
+// many floats from a bare device pointer, so a shorter tensor would be read
+// out of bounds (the reference asserts weights.len() == dst.len,
+// engine.rs:199).
+int check_f32(const slm_gguf* g, const std::string& name, uint64_t floats) {
+    slm_gguf_tensor t;
     const void* data;
     uint64_t bytes;
     int rc;
-    if ((rc = slm_gguf_tensor_data(g, name.c_str(), SLM_GGML_F32, &data, &bytes))) return rc;
+    if ((rc = slm_gguf_tensor_info(g, name.c_str(), &t)) ||
+        (rc = slm_gguf_tensor_data(g, name.c_str(), SLM_GGML_F32, &data, &bytes)))
+        return rc;
+    if (t.n_elements != floats || bytes != floats * 4)
+        return fail(nullptr, SLM_ERR_SHAPE,
+                    name + " holds " + std::to_string(t.n_elements) +
+                        " floats, the model dimension is " + std::to_string(floats));
+    return SLM_OK;
+}
+
+int check_q4(const slm_gguf* g, const std::string& name) {
+    const void* data;
+    uint64_t bytes;
+    return slm_gguf_tensor_data(g, name.c_str(), SLM_GGML_Q4_0, &data, &bytes);
+}
+
+// Every tensor the upload reads, checked before any device work: present,
+// of the right type and, for the norm vectors, dim floats long.
+int check_model_file(const slm_gguf* g, int num_layers, uint64_t dim) {
+    int rc;
+    if ((rc = check_q4(g, "token_embd.weight")) ||
+        (rc = check_f32(g, "output_norm.weight", dim)))
+        return rc;
+    slm_gguf_tensor out_info;
+    if (slm_gguf_tensor_info(g, "output.weight", &out_info) == SLM_OK &&
+        (rc = check_q4(g, "output.weight")))
+        return rc;
+    static const char* const q4_names[] = {"attn_q", "attn_k", "attn_v", "attn_output",
+                                           "ffn_gate", "ffn_up", "ffn_down"};
+    for (int l = 0; l < num_layers; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        if ((rc = check_f32(g, p + "attn_norm.weight", dim)) ||
+            (rc = check_f32(g, p + "ffn_norm.weight", dim)))
+            return rc;
+        for (const char* n : q4_names)
+            if ((rc = check_q4(g, p + n + ".weight"))) return rc;
+    }
+    return SLM_OK;
+}
+
+int load_f32(slm_model* m, const slm_gguf* g, const std::string& name, uint64_t floats,
+             const float** out) {
+    const void* data;
+    uint64_t bytes;
+    int rc;
+    if ((rc = check_f32(g, name, floats)) ||
+        (rc = slm_gguf_tensor_data(g, name.c_str(), SLM_GGML_F32, &data, &bytes)))
+        return rc;
     int prev = 0;
     if (hipGetDevice(&prev) != hipSuccess) prev = -1;
     float* d = nullptr;
     hipError_t e = hipSetDevice(m->device);
-    if (e == hipSuccess) e = hipMalloc(&d, bytes ? bytes : 4);
+    if (e == hipSuccess) e = hipMalloc(&d, bytes);
     if (e == hipSuccess) m->vecs.push_back(d);
-    if (e == hipSuccess && bytes) e = hipMemcpy(d, data, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d, data, bytes, hipMemcpyHostToDevice);
     if (prev >= 0) (void)hipSetDevice(prev);
     if (e != hipSuccess) return hip_fail(nullptr, e, "f32 tensor upload");
     *out = d;
@@ -70,23 +122,27 @@ int slm_model_load_gguf(const slm_gguf* g, int32_t device, int32_t num_layers,
     *out = nullptr;
     if (!g) return fail(nullptr, SLM_ERR_ARG, "gguf is NULL");
     if (num_layers < 1) return fail(nullptr, SLM_ERR_CONFIG, "num_layers must be positive");
-    slm_model* m = new slm_model();
-    m->device = device;
-    auto bail = [&](int rc) {
-        slm_model_destroy(m);
-        return rc;
-    };
     int rc;
     slm_gguf_tensor embd;
-    if ((rc = slm_gguf_tensor_info(g, "token_embd.weight", &embd))) return bail(rc);
+    if ((rc = slm_gguf_tensor_info(g, "token_embd.weight", &embd))) return rc;
     if (embd.dims[1] > INT32_MAX)
-        return bail(fail(nullptr, SLM_ERR_BOUNDS, "OutOfBounds(token_embd.weight)"));
+        return fail(nullptr, SLM_ERR_BOUNDS, "OutOfBounds(token_embd.weight)");
+    const uint64_t dim = embd.dims[0];  // the embedding width is the model dimension
+    if (dim == 0 || dim % 32 != 0)
+        return fail(nullptr, SLM_ERR_SHAPE, "token_embd.weight rows must be a multiple of 32 long");
+    if ((rc = check_model_file(g, num_layers, dim))) return rc;
+    slm_model* m = new slm_model();
+    m->device = device;
+    auto bail = [&](int code) {
+        slm_model_destroy(m);
+        return code;
+    };
     m->vocab = (int)embd.dims[1];
     const slm_q4_matrix* token_embd = nullptr;
     const slm_q4_matrix* lm_head = nullptr;
     const float* output_norm = nullptr;
     if ((rc = load_q4(m, g, "token_embd.weight", &token_embd)) ||
-        (rc = load_f32(m, g, "output_norm.weight", &output_norm)))
+        (rc = load_f32(m, g, "output_norm.weight", dim, &output_norm)))
         return bail(rc);
     slm_gguf_tensor out_info;
     if (slm_gguf_tensor_info(g, "output.weight", &out_info) == SLM_OK) {
@@ -98,12 +154,12 @@ int slm_model_load_gguf(const slm_gguf* g, int32_t device, int32_t num_layers,
     for (int l = 0; l < num_layers; ++l) {  // layer_weights (loader.rs:508-521)
         const std::string p = "blk." + std::to_string(l) + ".";
         slm_layer_weights& lw = m->layers[(size_t)l];
-        if ((rc = load_f32(m, g, p + "attn_norm.weight", &lw.rms_att)) ||
+        if ((rc = load_f32(m, g, p + "attn_norm.weight", dim, &lw.rms_att)) ||
             (rc = load_q4(m, g, p + "attn_q.weight", &lw.wq)) ||
             (rc = load_q4(m, g, p + "attn_k.weight", &lw.wk)) ||
             (rc = load_q4(m, g, p + "attn_v.weight", &lw.wv)) ||
             (rc = load_q4(m, g, p + "attn_output.weight", &lw.wo)) ||
-            (rc = load_f32(m, g, p + "ffn_norm.weight", &lw.rms_ffn)) ||
+            (rc = load_f32(m, g, p + "ffn_norm.weight", dim, &lw.rms_ffn)) ||
             (rc = load_q4(m, g, p + "ffn_gate.weight", &lw.w_gate)) ||
             (rc = load_q4(m, g, p + "ffn_up.weight", &lw.w_up)) ||
             (rc = load_q4(m, g, p + "ffn_down.weight", &lw.w_down)))

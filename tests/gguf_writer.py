@@ -107,16 +107,16 @@ def write_model(path, cfg: dict, w, tied: bool = False, arch: str = "llama",
         p = f"blk.{l}."
         h = lw.hidden_dim
         kvd = lw.wk.size // 18 * 32 // dim
-        g.add_tensor_f32(p + "attn_norm.weight", [dim], lw.rms_att)
+        g.add_tensor_f32(p + "attn_norm.weight", [len(lw.rms_att)], lw.rms_att)
         g.add_tensor_q4_0(p + "attn_q.weight", [dim, dim], lw.wq)
         g.add_tensor_q4_0(p + "attn_k.weight", [dim, kvd], lw.wk)
         g.add_tensor_q4_0(p + "attn_v.weight", [dim, kvd], lw.wv)
         g.add_tensor_q4_0(p + "attn_output.weight", [dim, dim], lw.wo)
-        g.add_tensor_f32(p + "ffn_norm.weight", [dim], lw.rms_ffn)
+        g.add_tensor_f32(p + "ffn_norm.weight", [len(lw.rms_ffn)], lw.rms_ffn)
         g.add_tensor_q4_0(p + "ffn_gate.weight", [dim, h], lw.w_gate)
         g.add_tensor_q4_0(p + "ffn_up.weight", [dim, h], lw.w_up)
         g.add_tensor_q4_0(p + "ffn_down.weight", [h, dim], lw.w_down)
-    g.add_tensor_f32("output_norm.weight", [dim], w.output_norm)
+    g.add_tensor_f32("output_norm.weight", [len(w.output_norm)], w.output_norm)
     if not tied:
         g.add_tensor_q4_0("output.weight", [dim, vocab], w.lm_head)
     g.write(path)

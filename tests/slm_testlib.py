@@ -3,6 +3,7 @@ loading of the product package (whose directory name has a hyphen)."""
 from __future__ import annotations
 
 import importlib.util
+import os
 import sys
 from dataclasses import dataclass
 from pathlib import Path
@@ -114,13 +115,50 @@ def err_stats(got, ref, atol=ATOL, rtol=RTOL):
     return float(diff.max(initial=0.0)), float(rel.max(initial=0.0))
 
 
+# |ref| above which the unfloored relative error is reported
+UNFLOORED_MIN = 1e-2
+
+
+def err_report(got, ref, atol=ATOL, rtol=RTOL) -> dict:
+    """max-abs, the floored max-rel of the bar (against max(|ref|, 0.1)), and
+    the unfloored max-rel over the elements with |ref| >= 1e-2, with the
+    largest |ref| for scale."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    diff = np.abs(got - ref)
+    big = np.abs(ref) >= UNFLOORED_MIN
+    return {
+        "max_abs": float(diff.max(initial=0.0)),
+        "max_rel": float((diff / np.maximum(np.abs(ref), atol / rtol)).max(initial=0.0)),
+        "max_rel_unfloored": float((diff[big] / np.abs(ref[big])).max(initial=0.0)),
+        "max_ref": float(np.abs(ref).max(initial=0.0)),
+    }
+
+
+# Worst errors per test, printed in the pytest summary (tests/conftest.py).
+WORST: dict = {}
+
+
+def _note(rep: dict) -> None:
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    w = WORST.setdefault(test, {"n": 0, "max_abs": 0.0, "max_rel": 0.0,
+                                "max_rel_unfloored": 0.0, "max_ref": 0.0})
+    w["n"] += 1
+    for k in ("max_abs", "max_rel", "max_rel_unfloored", "max_ref"):
+        w[k] = max(w[k], rep[k])
+
+
 def assert_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
     got = np.asarray(got)
     ref = np.asarray(ref)
     assert got.shape == ref.shape, (got.shape, ref.shape)
     assert np.all(np.isfinite(got)), f"{what}: non-finite values"
-    mabs, mrel = err_stats(got, ref, atol, rtol)
-    assert mabs <= atol and mrel <= rtol, f"{what}: max-abs {mabs:.3e} max-rel {mrel:.3e}"
+    rep = err_report(got, ref, atol, rtol)
+    _note(rep)
+    mabs, mrel = rep["max_abs"], rep["max_rel"]
+    assert mabs <= atol and mrel <= rtol, (
+        f"{what}: max-abs {mabs:.3e} max-rel {mrel:.3e} "
+        f"(unfloored {rep['max_rel_unfloored']:.3e} over |ref| >= {UNFLOORED_MIN})")
 
 
 def assert_bitwise(got, ref, what=""):

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from gguf_writer import (ARRAY, BOOL, F32, F64, GGML_F32, GGML_Q4_0, I8, I16, I32, I64, STR,
-                         U8, U16, U32, U64, GgufWriter, encode_value, gguf_str)
+                         U8, U16, U32, U64, GgufWriter, encode_value, gguf_str, write_model)
 from oracle import py_oracle as orc
 from slm_testlib import load_product
 
@@ -184,3 +184,56 @@ def test_model_config_from_metadata(tmp_path):
     assert c == {"dim": 256, "hidden_dim": 768, "num_heads": 8, "num_kv_heads": 8,
                  "max_seq_len": 64, "num_layers": 2, "rms_eps": np.float32(1e-5),
                  "rope_theta": 10000.0}
+
+
+def _ref_model_meta():
+    from test_oracle_layer import ref_model
+    cfg, w = ref_model()
+    meta = dict(dim=cfg.dim, hidden_dim=128, num_heads=cfg.num_heads,
+                num_kv_heads=cfg.num_kv_heads, max_seq_len=cfg.max_seq_len,
+                num_layers=cfg.num_layers, rms_eps=1e-5)
+    return cfg, w, meta
+
+
+@pytest.mark.parametrize("which", ["attn_norm", "ffn_norm", "output_norm"])
+def test_model_load_rejects_short_norm_before_upload(tmp_path, which):
+    # The norm kernels read dim floats from a bare device pointer; the
+    # reference asserts weights.len() == dst.len (engine.rs:199).  A cut-down
+    # norm tensor is refused with SLM_ERR_SHAPE while every tensor is checked,
+    # before any device allocation, copy or launch (this runs without a GPU).
+    import dataclasses
+    cfg, w, meta = _ref_model_meta()
+    short = np.ones(cfg.dim - 32, np.float32)
+    if which == "output_norm":
+        w = dataclasses.replace(w, output_norm=short)
+    else:
+        key = "rms_att" if which == "attn_norm" else "rms_ffn"
+        w = dataclasses.replace(w, layers=[dataclasses.replace(w.layers[0], **{key: short}),
+                                           w.layers[1]])
+    path = tmp_path / "short_norm.gguf"
+    write_model(path, meta, w)
+    with P.GgufFile(path) as f:
+        with pytest.raises(P.SlmAttnError) as ei:
+            P.GgufModel(f, meta["num_layers"])
+    assert ei.value.code == P.ERR_SHAPE
+    assert "dimension" in str(ei.value)
+
+
+def test_model_load_missing_tensor_and_wrong_type_before_upload(tmp_path):
+    # a missing layer and a tensor of the wrong type are found by the check
+    # pass before anything is uploaded (runs without a GPU)
+    cfg, w, meta = _ref_model_meta()
+    path = tmp_path / "model.gguf"
+    write_model(path, meta, w)
+    with P.GgufFile(path) as f:
+        with pytest.raises(P.SlmAttnError) as ei:   # asks for a third layer
+            P.GgufModel(f, 3)
+        assert ei.value.code == P.ERR_NOT_FOUND
+    g = GgufWriter()
+    g.add_tensor_f32("token_embd.weight", [cfg.dim, 4], np.zeros(4 * cfg.dim, np.float32))
+    path2 = tmp_path / "f32_embd.gguf"
+    g.write(path2)
+    with P.GgufFile(path2) as f:
+        with pytest.raises(P.SlmAttnError) as ei:
+            P.GgufModel(f, 1)
+        assert ei.value.code == P.ERR_TYPE

@@ -266,6 +266,26 @@ def test_error_codes_mirror_reference_asserts():
         with pytest.raises(P.SlmAttnError) as e:  # misaligned
             ctx.attend_dev(0, 0, base + 4, base + 8 * w.dim)
         assert e.value.code == P.ERR_ARG
+        # inputs of appending calls must not be cache rows: k taken from the
+        # row being appended would be rotated while other workgroups read it.
+        # Staging slots 4*dim floats apart (c1: kv_dim == dim), so only the KV
+        # overlap can be what is refused.
+        st = torch.zeros(16 * w.dim, device="cuda")
+        s0, s1, s2, s3 = (st.data_ptr() + 4 * i * 4 * w.dim for i in range(4))
+        kv = ctx.kv_device_ptr()
+        row3 = kv + 4 * ctx.kv_offset(0, 0, 3)
+        with pytest.raises(P.SlmAttnError) as e:  # decode, k = K row 3
+            ctx.decode_dev(0, 3, s0, row3, s2, s3)
+        assert e.value.code == P.ERR_ALIAS and "KV cache" in e.value.message
+        with pytest.raises(P.SlmAttnError) as e:  # decode, q inside the region
+            ctx.decode_dev(0, 3, row3, s1, s2, s3)
+        assert e.value.code == P.ERR_ALIAS and "KV cache" in e.value.message
+        with pytest.raises(P.SlmAttnError) as e:  # prefill, v = V rows 0..1
+            ctx.prefill_dev(0, 0, 2, s0, s1, kv + 4 * ctx.kv_offset(0, 1, 0), s3)
+        assert e.value.code == P.ERR_ALIAS and "KV cache" in e.value.message
+        with pytest.raises(P.SlmAttnError) as e:  # KV append from a cache row
+            ctx.kv_append_dev(0, 5, 1, row3, s2)
+        assert e.value.code == P.ERR_ALIAS and "KV cache" in e.value.message
         with pytest.raises(P.SlmAttnError) as e:
             ctx.kv_write(0, 2, 0, k)
         assert e.value.code == P.ERR_ARG
