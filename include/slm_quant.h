@@ -71,6 +71,23 @@ int slm_attn_decode_xb_dev(slm_attn_ctx* ctx, int32_t layer, int32_t pos, const 
                            const slm_q4_matrix* wq, const slm_q4_matrix* wk,
                            const slm_q4_matrix* wv, float* out);
 
+/* slm_attn_decode_xb_dev without any device allocation, for callers that
+ * cannot allocate (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference: its GEMVs write
+ * into the caller's arena.  q, k, v and the decode split partials live in a
+ * file-scope device array of 1 MiB (262144 floats) that each GPU holds until
+ * the process ends; a call needs dim + 2*kv_dim + n_splits*num_heads*
+ * (head_dim + 2) floats of it (n_splits from slm_attn_decode_splits at pos +
+ * 1) and returns SLM_ERR_SHAPE above that.  Every call on a GPU shares that
+ * GPU's array and nothing in it needs clearing: calls that overlap on one
+ * GPU (two streams, two contexts) race and must be ordered by the caller.
+ * Not timed by slm_attn_profile.  Results are identical to
+ * slm_attn_decode_xb_dev's. */
+int slm_attn_decode_xb_dev_noalloc(slm_attn_ctx* ctx, int32_t layer, int32_t pos,
+                                   const float* xb, const slm_q4_matrix* wq,
+                                   const slm_q4_matrix* wk, const slm_q4_matrix* wv,
+                                   float* out);
+
 /* The prefill attention block of forward_batch_with_kv from n rows of the
  * attention RMSNorm output (transformer.rs:530-593): the three GEMMs, then
  * slm_attn_prefill_dev for rows start..start+n-1. */

@@ -151,6 +151,7 @@ SIGNATURES = {
     "slm_quantize_q8_0_dev": (ctypes.c_int, [_P, _P, ctypes.c_int64, _P]),
     "slm_gemm_q4_0_dev": (ctypes.c_int, [_P, _P, _P, _I, _P]),
     "slm_attn_decode_xb_dev": (ctypes.c_int, [_P, _I, _I, _P, _P, _P, _P, _P]),
+    "slm_attn_decode_xb_dev_noalloc": (ctypes.c_int, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "slm_attn_prefill_xb_dev": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _P, _P, _P]),
     "slm_gemm_q4_0_residual_dev": (ctypes.c_int, [_P, _P, _P, _I, _P, _P]),
     "slm_attn_decode_wo_dev": (ctypes.c_int, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
@@ -372,6 +373,11 @@ class AttentionContext:
                       out) -> None:
         self._check(self.lib.slm_attn_decode_xb_dev(self._h, layer, pos, xb, wq.handle,
                                                     wk.handle, wv.handle, out))
+
+    def decode_xb_dev_noalloc(self, layer, pos, xb, wq: "Q4Matrix", wk: "Q4Matrix",
+                              wv: "Q4Matrix", out) -> None:
+        self._check(self.lib.slm_attn_decode_xb_dev_noalloc(self._h, layer, pos, xb, wq.handle,
+                                                            wk.handle, wv.handle, out))
 
     def prefill_xb_dev(self, layer, start, n, xb, wq: "Q4Matrix", wk: "Q4Matrix",
                        wv: "Q4Matrix", out) -> None:

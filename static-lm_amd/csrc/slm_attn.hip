@@ -7,12 +7,50 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "slm_host.h"
 
+// Scratch of slm_attn_decode_xb_dev_noalloc: q | k | v rows of one token,
+// then the decode split partials.  Every device the library runs on holds
+// its own copy until the process ends; host code uses the per-device
+// address hipGetSymbolAddress gives, never the symbol itself.
+constexpr size_t kNoAllocScratchFloats = size_t(1) << 18;  // 1 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
 namespace slm_host {
+
+namespace {
+
+// Address of `scratch` on each device, taken once per device with that
+// device current (the first slm_attn_create on it).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+std::string g_scratch_err[kMaxDevices];
+
+float* noalloc_scratch_on(int dev, std::string* why) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        *why = "device index above the no-allocation table";
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev] && g_scratch_err[dev].empty()) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+            g_scratch_err[dev] = std::string("hipGetSymbolAddress(scratch): ") +
+                                 hipGetErrorString(e);
+        else
+            g_scratch_ptr[dev] = static_cast<float*>(ptr);
+    }
+    *why = g_scratch_err[dev];
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
 
 thread_local std::string g_last_error;
 
@@ -204,8 +242,9 @@ int do_append(slm_attn_ctx* c, int layer, int pos0, int n, const float* k,
 // Single-token decode at pos: with k_new/v_new the KV row is appended and q
 // is rotated at pos inside the kernel; without them q is already rotated and
 // row pos is read from the cache.
-int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* k_new,
-              const float* v_new, float* out, bool rotate) {
+int do_decode_in(slm_attn_ctx* c, int layer, int pos, const float* q, const float* k_new,
+                 const float* v_new, float* out, bool rotate, float* part_o, float* part_ml,
+                 bool timed) {
     const slm::Shape& s = c->shape;
     int ns = 1, tile = 1;
     slm::decode_split_policy(s, pos + 1, &ns, &tile);
@@ -217,10 +256,17 @@ int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* 
                       rotate ? c->cos_t : nullptr,
                       rotate ? c->sin_t : nullptr,
                       out,
-                      c->part_o,
-                      c->part_ml,
+                      part_o,
+                      part_ml,
                       pos,
                       ns};
+    if (!timed) {
+        hipError_t e = slm::launch_decode(s, a, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "decode kernel launch");
+        if (ns == 1) return SLM_OK;
+        return launch_status(c, slm::launch_decode_combine(s, a, c->stream),
+                             "decode combine kernel launch");
+    }
     {
         // the launch stamps the events at the kernel's own start and end
         Timed t(c, SLM_K_DECODE, /*in_launch=*/true);
@@ -237,6 +283,12 @@ int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* 
     hipError_t e = slm::launch_decode_combine(s, a, c->stream);
     t.done_in_launch(e == hipSuccess);
     return launch_status(c, e, "decode combine kernel launch");
+}
+
+int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* k_new,
+              const float* v_new, float* out, bool rotate) {
+    return do_decode_in(c, layer, pos, q, k_new, v_new, out, rotate, c->part_o, c->part_ml,
+                        true);
 }
 
 // Attention of rows b < n at positions start + b over cache rows 0..start+b.
@@ -505,6 +557,9 @@ int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
         e = hipMalloc(&c->part_ml,
                       (size_t)max_splits * s.num_heads * 2 * sizeof(float));
     if (e != hipSuccess) return bail(hip_fail(nullptr, e, "hipMalloc(decode partials)"));
+    // set-up of the no-allocation entry point on this device (the context's
+    // own calls never need it, so a failure only disables that entry point)
+    c->noalloc_scratch = noalloc_scratch_on(dev, &c->noalloc_err);
 
     *out = c;
     return SLM_OK;
@@ -920,6 +975,50 @@ int slm_attn_decode_xb_dev(slm_attn_ctx* c, int32_t layer, int32_t pos, const fl
     if (overlaps(out, (size_t)s.dim * 4, c->qkv, c->qkv_floats * 4))
         return fail(c, SLM_ERR_ALIAS, "out must not overlap the context's buffers");
     return do_decode(c, layer, pos, q, k, v, out, true);
+}
+
+int slm_attn_decode_xb_dev_noalloc(slm_attn_ctx* c, int32_t layer, int32_t pos,
+                                   const float* xb, const slm_q4_matrix* wq,
+                                   const slm_q4_matrix* wk, const slm_q4_matrix* wv,
+                                   float* out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    const slm::Shape& s = c->shape;
+    int rc;
+    if ((rc = check_layer(c, layer)) || (rc = check_pos(c, pos)) ||
+        (rc = check_dev_ptrs(c, {xb, out})) ||
+        (rc = check_out_alias(c, out, s.dim, {{xb, s.dim}}, true)))
+        return rc;
+    if (!c->noalloc_scratch)
+        return fail(c, SLM_ERR_HIP, "no-allocation scratch unavailable on this device: " +
+                                        c->noalloc_err);
+    // scratch layout: q [dim] | k [kv_dim] | v [kv_dim] | partials of the
+    // split count at pos + 1 (o [n_splits][num_heads][head_dim], then
+    // (max, sum) [n_splits][num_heads][2]); every segment 16-byte aligned
+    int ns = 1, tile = 1;
+    slm::decode_split_policy(s, pos + 1, &ns, &tile);
+    const size_t rows = (size_t)s.dim + 2 * (size_t)s.kv_dim;  // multiple of 32
+    const size_t po = (size_t)ns * s.num_heads * s.head_dim;
+    const size_t need = rows + po + (size_t)ns * s.num_heads * 2;
+    if (need > kNoAllocScratchFloats)
+        return fail(c, SLM_ERR_SHAPE,
+                    "this shape and position need " + std::to_string(need) +
+                        " floats of no-allocation scratch; the maximum is " +
+                        std::to_string(kNoAllocScratchFloats));
+    if ((rc = check_matrix(c, wq, s.dim, s.dim, "wq")) ||
+        (rc = check_matrix(c, wk, s.kv_dim, s.dim, "wk")) ||
+        (rc = check_matrix(c, wv, s.kv_dim, s.dim, "wv")))
+        return rc;
+    if (overlaps(out, (size_t)s.dim * 4, c->noalloc_scratch, kNoAllocScratchFloats * 4))
+        return fail(c, SLM_ERR_ALIAS, "out must not overlap the library's scratch");
+    float* q = c->noalloc_scratch;
+    float* k = q + s.dim;
+    float* v = k + s.kv_dim;
+    float* part_o = q + rows;
+    float* part_ml = part_o + po;
+    const slm::Q4Job jobs[3] = {q4_job(wq, q), q4_job(wk, k), q4_job(wv, v)};
+    hipError_t e = slm::launch_q4_gemv(jobs, 3, xb, s.dim / 32, 1, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "q4 gemv kernel launch");
+    return do_decode_in(c, layer, pos, q, k, v, out, true, part_o, part_ml, false);
 }
 
 int slm_attn_prefill_xb_dev(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t n,

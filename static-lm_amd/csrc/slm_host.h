@@ -42,6 +42,10 @@ struct slm_attn_ctx {
     float* part_o = nullptr;
     float* part_ml = nullptr;
     int max_splits = 1;
+    // this device's copy of the file-scope scratch of the no-allocation
+    // entry point (nullptr when its address could not be taken)
+    float* noalloc_scratch = nullptr;
+    std::string noalloc_err;
     // staging for the host-pointer entry points
     float* stage = nullptr;
     size_t stage_floats = 0;
@@ -182,6 +186,11 @@ int launch_status(slm_attn_ctx* c, hipError_t e, const char* what);
 int do_append(slm_attn_ctx* c, int layer, int pos0, int n, const float* k, const float* v);
 int do_decode(slm_attn_ctx* c, int layer, int pos, const float* q, const float* k_new,
               const float* v_new, float* out, bool rotate);
+// The same with the split partials in part_o / part_ml and, when timed is
+// false, no profiling events taken.
+int do_decode_in(slm_attn_ctx* c, int layer, int pos, const float* q, const float* k_new,
+                 const float* v_new, float* out, bool rotate, float* part_o, float* part_ml,
+                 bool timed);
 int do_attend(slm_attn_ctx* c, int layer, int start, int n, const float* q, float* out,
               bool rotate);
 int ensure_q8(slm_attn_ctx* c, size_t n, int nb);
