@@ -80,6 +80,27 @@ def measured_traffic() -> int | None:
     return None
 
 
+PREFILL_PROFILE = REPO / "profiles" / "prefill_mfma_kernel_llama3-8b_4096.md"
+
+
+def prefill_profile() -> dict:
+    """MFMA-busy fraction and LDS counters of the 4096-row prefill kernel from
+    the committed rocprofv3 summary (empty when it is absent)."""
+    out = {}
+    try:
+        for ln in PREFILL_PROFILE.read_text().splitlines():
+            for key in ("mfma_busy_frac", "lds_bank_conflict_cycles", "lds_instructions",
+                        "trace_median_ms"):
+                if ln.startswith(key + "(prefill_mfma_kernel 4096):"):
+                    v = ln.split(":", 1)[1].strip()
+                    out[key] = float(v) if "." in v else int(v)
+    except OSError:
+        pass
+    if out:
+        out["counters_source"] = PREFILL_PROFILE.name
+    return out
+
+
 def host_cpu() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -153,6 +174,12 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
     achieved = kv_bytes / avg_split_s / 1e9
     ns, tile = ctx.decode_splits(pos + 1)
     finite = bool(torch.isfinite(out).all().item())
+    # what the oracle needs to replay layer 0 of the timed configuration: its
+    # cache rows before the step, q, k, v, and the GPU's output and appended row
+    check = {"pos": pos, "k_rows": ctx.kv_read(0, 0, 0, pos), "v_rows": ctx.kv_read(0, 1, 0, pos),
+             "q": q[0].cpu().numpy(), "k": k[0].cpu().numpy(), "v": v[0].cpu().numpy(),
+             "out": out[0].cpu().numpy(), "k_row": ctx.kv_read(0, 0, pos, 1)[0],
+             "v_row": ctx.kv_read(0, 1, pos, 1)[0]}
     ctx.close()
     step_bytes = layers * decode_bytes(pos)
     return {
@@ -162,6 +189,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
         "split_kernel_bytes": kv_bytes, "split_kernel_gbs": achieved,
         "splits": ns, "tile": tile, "finite": finite,
         "combine_avg_us": comb_ms / max(n_comb, 1) * 1e3,
+        "_check": check,
     }
 
 
@@ -540,7 +568,7 @@ def bench_decode_131k(torch, P) -> dict:
             "gbs": total / (ms / 1e3) / 1e9}
 
 
-# The BASELINE.json configurations: (name, dim, heads, kv_heads, hd, layers, max_seq_len,
+# The five workload configurations: (name, dim, heads, kv_heads, layers, max_seq_len,
 # theta, prefill rows, decode steps, pre-filled rows)
 WORKLOADS = [
     ("c1 synthetic dim256 4/4 hd64 2L msl512", 256, 4, 4, 2, 512, 1e4, 16, 8, 0),
@@ -551,22 +579,48 @@ WORKLOADS = [
 ]
 
 
-def bench_workloads(torch, P) -> list:
+def workload_inputs(ci: int, dim: int, kvd: int, layers: int, rows: int):
+    """Seeded N(0,1)*0.5 f32 q, k, v per layer: [layers][rows][dim | kv_dim]."""
+    rng = np.random.default_rng(0x5EED0000 + ci)
+    half = np.float32(0.5)
+    q = rng.standard_normal((layers, rows, dim), dtype=np.float32) * half
+    k = rng.standard_normal((layers, rows, kvd), dtype=np.float32) * half
+    v = rng.standard_normal((layers, rows, kvd), dtype=np.float32) * half
+    return q, k, v
+
+
+def prefilled_cache(ci: int, rows: int, kvd: int):
+    """Seeded raw K and V cache rows 0..rows-1 (layer 0) for a pre-filled workload."""
+    rng = np.random.default_rng(0x5EED1000 + ci)
+    half = np.float32(0.5)
+    kc = rng.standard_normal((rows, kvd), dtype=np.float32) * half
+    vc = rng.standard_normal((rows, kvd), dtype=np.float32) * half
+    return kc, vc
+
+
+def bench_workloads(torch, P) -> tuple[list, list]:
     """Each configuration end to end on device pointers: per layer one prefill
-    of P rows then D decode steps, timed once after one untimed pass."""
-    out = []
-    for name, dim, h, kvh, layers, msl, theta, npf, nd, pre in WORKLOADS:
+    of P rows then D decode steps.  Reports the host-bound wall time of a pass
+    (one Python call per launch) next to the kernels' own time (launch-stamped
+    decode and merge events, events around the other launches), with the
+    algorithmic rates and roofline fractions of the prefill and decode kernels.
+    Also returns, per configuration, the inputs, outputs and appended cache
+    rows of the last pass, for the oracle comparison of the CPU baseline leg."""
+    out, checks = [], []
+    stream = torch.cuda.current_stream()
+    for ci, (name, dim, h, kvh, layers, msl, theta, npf, nd, pre) in enumerate(WORKLOADS, 1):
         hd = dim // h
         kvd = hd * kvh
-        ctx = P.AttentionContext(dim, h, kvh, msl, layers, theta)
-        stream = torch.cuda.current_stream()
-        ctx.set_stream(stream.cuda_stream)
-        if pre:
-            fill_cache(torch, ctx, layers, msl, pre, 7)
         rows = npf + nd
-        q = torch.randn(layers, rows, dim, device="cuda") * 0.5
-        k = torch.randn(layers, rows, kvd, device="cuda") * 0.5
-        v = torch.randn(layers, rows, kvd, device="cuda") * 0.5
+        ctx = P.AttentionContext(dim, h, kvh, msl, layers, theta)
+        ctx.set_stream(stream.cuda_stream)
+        qh, kh, vh = workload_inputs(ci, dim, kvd, layers, rows)
+        pre_k = pre_v = None
+        if pre:
+            pre_k, pre_v = prefilled_cache(ci, pre, kvd)
+            ctx.kv_write(0, 0, 0, pre_k)
+            ctx.kv_write(0, 1, 0, pre_v)
+        q, k, v = (torch.from_numpy(a).cuda() for a in (qh, kh, vh))
         o = torch.empty(layers, rows, dim, device="cuda")
 
         def run():
@@ -586,49 +640,186 @@ def bench_workloads(torch, P) -> list:
         run()
         e1.record(stream)
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1)
+        wall_ms = e0.elapsed_time(e1)
+        ctx.profile(True)
+        run()
+        prof = ctx.profile_read()
+        ctx.profile(False)
         flops = layers * 4 * hd * h * sum(range(pre + 1, pre + npf + 1))
         dec_bytes = layers * sum(4 * (2 * (p + 1) * kvd + 2 * dim + 4 * kvd)
                                  for p in range(pre + npf, pre + npf + nd))
-        out.append({"workload": name, "gpu_ms": round(ms, 4), "prefill_flops": flops,
-                    "decode_bytes": dec_bytes, "launches": layers * ((1 if npf else 0) + nd)})
+        kern = {kind: round(ms, 4) for kind, (cnt, ms) in prof.items() if cnt}
+        pf_ms = prof["prefill"][1] + prof["append"][1]
+        dec_ms = prof["decode"][1] + prof["combine"][1]
+        rec = {"workload": name, "wall_ms": round(wall_ms, 4),
+               "kernel_ms": round(sum(ms for _, ms in prof.values()), 4),
+               "kernel_ms_by_kind": kern,
+               "launches": int(sum(cnt for cnt, _ in prof.values())),
+               "prefill_flops": flops, "decode_bytes": dec_bytes}
+        if npf:
+            rec["prefill_tflops"] = round(flops / (pf_ms / 1e3) / 1e12, 3)
+            rec["prefill_frac_fp32_mfma"] = round(flops / (pf_ms / 1e3) / 1e12
+                                                  / FP32_MFMA_PEAK_TFLOPS, 4)
+        rec["decode_gbs"] = round(dec_bytes / (dec_ms / 1e3) / 1e9, 1)
+        rec["decode_frac_hbm"] = round(dec_bytes / (dec_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
+        rec["kernel_frac_of_wall"] = round(rec["kernel_ms"] / wall_ms, 3)
+        out.append(rec)
+        got = o.cpu().numpy()
+        kv_rows = [(ctx.kv_read(l, 0, pre, rows), ctx.kv_read(l, 1, pre, rows))
+                   for l in range(layers)]
+        checks.append({"cfg": (dim, h, kvh, msl, layers, theta), "npf": npf, "nd": nd, "pre": pre,
+                       "q": qh, "k": kh, "v": vh, "out": got, "kv": kv_rows,
+                       "pre_k": pre_k, "pre_v": pre_v})
         ctx.close()
         del q, k, v, o
-    return out
+    return out, checks
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """The oracle's decode (rope + append + JIT-softmax attention) at position
-    32767 of one layer of the same shape, on one host core, repeated until
-    the time budget is spent; plus a sample of prefill rows."""
+def _errs(got, ref) -> dict:
+    """max-abs; max-rel floored at |ref| = 0.1 (the parity bar's 1e-4 / 1e-3);
+    unfloored max-rel over |ref| >= 1e-2."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    d = np.abs(got - ref)
+    big = np.abs(ref) >= 1e-2
+    return {"max_abs": float(d.max(initial=0.0)),
+            "max_rel": float((d / np.maximum(np.abs(ref), 0.1)).max(initial=0.0)),
+            "max_rel_unfloored": float((d[big] / np.abs(ref[big])).max(initial=0.0)),
+            "n": int(d.size)}
+
+
+def _merge_errs(a: dict | None, b: dict) -> dict:
+    if a is None:
+        return dict(b)
+    return {k: (a[k] + b[k] if k == "n" else max(a[k], b[k])) for k in b}
+
+
+def _bitwise(a, b) -> bool:
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
+
+
+def cpu_configs(checks: list) -> list:
+    """CPU baseline leg for the configurations: the oracle (the reference's
+    single-threaded attention arithmetic restated in C, one host core) on the
+    same inputs as the GPU run, timed, and used as the checker of the GPU
+    outputs and appended cache rows.  C1-C3 run in full; C4 times its prefill
+    on 24 rows spread over the 4096 and 4 of its 128 decode steps, C5 3 of its
+    64 decode steps (the other rows are appended to the oracle's cache
+    untimed), and the full-run CPU time is extrapolated by flops / bytes."""
     sys.path.insert(0, str(REPO))
     from oracle import py_oracle as orc
 
-    ctx_len = 32768
-    pos = ctx_len - 1
-    cfg = orc.Cfg(DIM, HEADS, KV_HEADS, ctx_len, 1, THETA)
+    res = []
+    for ch in checks:
+        dim, h, kvh, msl, layers, theta = ch["cfg"]
+        cfg = orc.Cfg(dim, h, kvh, msl, layers, theta)
+        hd, kvd = dim // h, dim // h * kvh
+        npf, nd, pre = ch["npf"], ch["nd"], ch["pre"]
+        q, k, v, got = ch["q"], ch["k"], ch["v"], ch["out"]
+        om = orc.OracleModel(cfg)
+        if pre:
+            om.k_cache(0)[:pre] = ch["pre_k"]
+            om.v_cache(0)[:pre] = ch["pre_v"]
+        full = pre == 0 and npf <= 1024  # C1-C3
+        err, t_oracle = None, 0.0
+        est_ms, sample = None, "full run"
+        if full:
+            for l in range(layers):
+                if npf:
+                    t0 = time.perf_counter()
+                    r = om.prefill(l, pre, q[l, :npf], k[l, :npf], v[l, :npf])
+                    t_oracle += time.perf_counter() - t0
+                    err = _merge_errs(err, _errs(got[l, :npf], r))
+                for st in range(nd):
+                    p = pre + npf + st
+                    t0 = time.perf_counter()
+                    r = om.decode(l, p, q[l, npf + st], k[l, npf + st], v[l, npf + st])
+                    t_oracle += time.perf_counter() - t0
+                    err = _merge_errs(err, _errs(got[l, npf + st], r))
+            est_ms = t_oracle * 1e3
+        else:
+            f_all = f_smp = b_all = b_smp = 0.0
+            t_pf = t_dec = 0.0
+            if npf:
+                om.append(0, pre, k[0, :npf], v[0, :npf])
+                rows = sorted(set(np.linspace(0, npf - 1, 24).astype(int).tolist()))
+                for b in rows:
+                    t0 = time.perf_counter()
+                    r = om.attend(0, q[0, b], pre + b)
+                    t_pf += time.perf_counter() - t0
+                    f_smp += 4 * hd * h * (pre + b + 1)
+                    err = _merge_errs(err, _errs(got[0, b], r))
+                f_all = 4 * hd * h * sum(range(pre + 1, pre + npf + 1))
+            steps = sorted({0, 1, nd // 2, nd - 1} if npf else {0, 1, nd - 1})
+            for st in range(nd):
+                p = pre + npf + st
+                bp = 4 * (2 * (p + 1) * kvd + 2 * dim + 4 * kvd)
+                b_all += bp
+                if st in steps:
+                    t0 = time.perf_counter()
+                    r = om.decode(0, p, q[0, npf + st], k[0, npf + st], v[0, npf + st])
+                    t_dec += time.perf_counter() - t0
+                    b_smp += bp
+                    err = _merge_errs(err, _errs(got[0, npf + st], r))
+                else:
+                    om.append(0, p, k[0, npf + st], v[0, npf + st])
+            t_oracle = t_pf + t_dec
+            est_ms = ((t_pf * f_all / f_smp if f_smp else 0.0) + t_dec * b_all / b_smp) * 1e3
+            sample = ((f"prefill rows {rows[0]}..{rows[-1]} ({len(rows)} of {npf}) and " if npf
+                       else "") + f"decode steps {steps} of {nd}, extrapolated by flops / bytes")
+        kv_ok = all(_bitwise(ch["kv"][l][0], om.k_cache(l)[pre:pre + npf + nd]) and
+                    _bitwise(ch["kv"][l][1], om.v_cache(l)[pre:pre + npf + nd])
+                    for l in range(layers))
+        res.append({"cpu_ms": round(est_ms, 3), "cpu_sample_s": round(t_oracle, 3),
+                    "cpu_sample": sample, "cores": 1,
+                    "parity": {**{k2: (round(v2, 10) if isinstance(v2, float) else v2)
+                                  for k2, v2 in err.items()},
+                               "kv_bitwise": kv_ok,
+                               "pass": bool(kv_ok and err["max_abs"] <= 1e-4
+                                            and err["max_rel"] <= 1e-3)}})
+        del om
+    return res
+
+
+def cpu_baseline(budget_s: float, hc: dict) -> dict:
+    """The oracle's decode (rope + append + JIT-softmax attention) of the
+    headline workload -- one layer at position 32767 over the same cache rows,
+    q, k and v as the GPU run's layer 0 -- on one host core, repeated until
+    the time budget is spent; its output checks the GPU's (parity of the timed
+    configuration).  Plus a sample of prefill rows of a 4096-token prefill."""
+    sys.path.insert(0, str(REPO))
+    from oracle import py_oracle as orc
+
+    pos = hc["pos"]
+    cfg = orc.Cfg(DIM, HEADS, KV_HEADS, pos + 1, 1, THETA)
     om = orc.OracleModel(cfg)
-    rng = np.random.default_rng(5)
-    om.k_cache(0)[:] = rng.standard_normal((ctx_len, KV_DIM), dtype=np.float32) * 0.5
-    om.v_cache(0)[:] = rng.standard_normal((ctx_len, KV_DIM), dtype=np.float32) * 0.5
-    q = rng.standard_normal(DIM, dtype=np.float32) * 0.5
-    k = rng.standard_normal(KV_DIM, dtype=np.float32) * 0.5
-    v = rng.standard_normal(KV_DIM, dtype=np.float32) * 0.5
+    om.k_cache(0)[:pos] = hc["k_rows"]
+    om.v_cache(0)[:pos] = hc["v_rows"]
     calls = 0
     t0 = time.perf_counter()
     while True:
-        om.decode(0, pos, q, k, v)
+        r = om.decode(0, pos, hc["q"], hc["k"], hc["v"])
         calls += 1
         el = time.perf_counter() - t0
         if el >= budget_s * 0.75:
             break
     dec_gbs = decode_bytes(pos) * calls / el / 1e9
+    parity = _errs(hc["out"], r)
+    parity["kv_bitwise"] = (_bitwise(hc["k_row"], om.k_cache(0)[pos])
+                            and _bitwise(hc["v_row"], om.v_cache(0)[pos]))
+    parity["pass"] = bool(parity["kv_bitwise"] and parity["max_abs"] <= 1e-4
+                          and parity["max_rel"] <= 1e-3)
+    del om
     # prefill sample: the last rows of a 4096-token prefill, each attending
     # to 4090+ cached rows (the per-row loop of the reference)
+    rng = np.random.default_rng(5)
     pcfg = orc.Cfg(DIM, HEADS, KV_HEADS, 4096, 1, THETA)
     pm = orc.OracleModel(pcfg)
     pm.k_cache(0)[:] = rng.standard_normal((4096, KV_DIM), dtype=np.float32) * 0.5
     pm.v_cache(0)[:] = rng.standard_normal((4096, KV_DIM), dtype=np.float32) * 0.5
+    q = rng.standard_normal(DIM, dtype=np.float32) * 0.5
     rows = 0
     flops = 0
     t1 = time.perf_counter()
@@ -642,8 +833,9 @@ def cpu_baseline(budget_s: float) -> dict:
             break
     return {
         "value": dec_gbs, "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": f"{calls} oracle decode calls (rope+append+attention) at pos {pos}, one layer, "
-                  f"{el:.1f} s on {host_cpu()} (nproc {os.cpu_count()})",
+        "sample": f"{calls} oracle decode calls (rope+append+attention) at pos {pos} on layer 0 "
+                  f"of the headline cache, {el:.1f} s on {host_cpu()} (nproc {os.cpu_count()})",
+        "parity": parity,
         "prefill_tflops": flops / el2 / 1e12,
         "prefill_sample": f"last {rows} rows of a 4096-token prefill, {el2:.1f} s",
     }
@@ -654,7 +846,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-seconds", type=float, default=16.0,
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of the CPU baseline sample (0 skips it)")
     ap.add_argument("--skip-extra", action="store_true",
                     help="only the headline decode @32k measurement")
@@ -741,7 +933,7 @@ def main() -> int:
         log("decode @131k")
         dl = bench_decode_131k(torch, P)
         log("all configurations")
-        wl = bench_workloads(torch, P)
+        wl, wl_checks = bench_workloads(torch, P)
         log(f"decode @131k: {dl['ms_per_step']*1e3:.1f} us/step, {dl['gbs']:.1f} GB/s")
         log("attention block from xb")
         bx = bench_block_xb(torch, P, max(3, args.steps // 5))
@@ -755,19 +947,34 @@ def main() -> int:
         bm = bench_model(torch, P)
         log(f"model: prefill {bm['prefill_tokens_per_s']:.0f} tokens/s, decode "
             f"{bm['decode_tokens_per_s']:.1f} tokens/s ({bm['decode_ms_per_token']:.2f} ms/token)")
-        log("calibration")
+        log("measurement probes")
         cal_mfma = P.calibrate_mfma_f32(iters=20000)
         cal_nt = P.calibrate_hbm_read(4 << 30, nontemporal=True)
         cal_plain = P.calibrate_hbm_read(4 << 30, nontemporal=False)
-        log(f"calibration: fp32 MFMA {cal_mfma['tflops']:.1f} TFLOP/s, HBM read "
+        log(f"probes: fp32 MFMA {cal_mfma['tflops']:.1f} TFLOP/s, streaming read "
             f"{cal_nt:.0f} GB/s nontemporal, {cal_plain:.0f} GB/s plain")
+        pf_prof = prefill_profile()
         extra = {
-            "calibration": {
+            "roofline_prefill": {
+                "bound": "mfma",
+                "kernel": "prefill_mfma_kernel<128,4,1,1> (causal attention, fp32 "
+                          "v_mfma_f32_16x16x4f32, 4096 rows)",
+                "achieved": round(pf["kernel_tflops"], 2),
+                "peak": FP32_MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(pf["kernel_tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
+                "avg_launch_ms": round(pf["kernel_avg_ms"], 4),
+                "algorithmic_flops_per_launch": pf["flops"],
+                **pf_prof,
+            },
+            "probes": {
                 "mfma_f32_16x16x4_tflops": round(cal_mfma["tflops"], 2),
-                "hbm_read_nontemporal_gbs": round(cal_nt, 1),
-                "hbm_read_plain_gbs": round(cal_plain, 1),
-                "note": "measured ceilings on this device (slm_calib.h); roofline.peak stays "
-                        "the published figure",
+                "stream_read_nontemporal_gbs": round(cal_nt, 1),
+                "stream_read_plain_gbs": round(cal_plain, 1),
+                "note": "plain streaming-read and MFMA-chain probes on this device "
+                        "(libslm_calib.so); not ceilings of the product kernels (the 131k "
+                        "decode streams faster than the read probe); roofline peaks are the "
+                        "published figures",
             },
             "prefill_4k": {
                 "tflops": pf["tflops"], "ms": pf["ms"], "flops": pf["flops"],
@@ -788,7 +995,15 @@ def main() -> int:
     cpu = None
     if args.cpu_seconds > 0:
         log("cpu baseline")
-        cpu = cpu_baseline(args.cpu_seconds)
+        cpu = cpu_baseline(args.cpu_seconds, d["_check"])
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s; headline parity max-abs "
+            f"{cpu['parity']['max_abs']:.2e}, KV bitwise {cpu['parity']['kv_bitwise']}")
+        if not args.skip_extra:
+            log("cpu baseline of the configurations (oracle on the same inputs)")
+            for rec, c in zip(extra["configs"], cpu_configs(wl_checks)):
+                rec.update(c)
+                log(f"{rec['workload']}: cpu {c['cpu_ms']:.1f} ms ({c['cpu_sample']}), "
+                    f"max-abs {c['parity']['max_abs']:.2e}, KV bitwise {c['parity']['kv_bitwise']}")
 
     ms_per_step = d["ms"] / d["steps"]
     res = {
@@ -826,6 +1041,7 @@ def main() -> int:
             "algorithmic_bytes_per_launch": d["split_kernel_bytes"],
         },
         "cpu_baseline": cpu,
+        "parity": cpu["parity"] if cpu else None,
         "frac_hbm_step": round(d["gbs"] / HBM_PEAK_GBS, 4),
         **extra,
     }

@@ -24,7 +24,8 @@ import numpy as np
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libslm_attn.so"
 HEADER_PATH = PKG_DIR.parent / "include" / "slm_attn.h"
-CALIB_HEADER_PATH = PKG_DIR.parent / "include" / "slm_calib.h"
+CALIB_HEADER_PATH = PKG_DIR / "calib" / "slm_calib.h"
+CALIB_LIB_PATH = PKG_DIR / "calib" / "libslm_calib.so"
 QUANT_HEADER_PATH = PKG_DIR.parent / "include" / "slm_quant.h"
 LAYER_HEADER_PATH = PKG_DIR.parent / "include" / "slm_layer.h"
 GGUF_HEADER_PATH = PKG_DIR.parent / "include" / "slm_gguf.h"
@@ -139,11 +140,6 @@ SIGNATURES = {
     "slm_attn_profile_read": (ctypes.c_int, [_P, ctypes.POINTER(_KernelStat)]),
     "slm_attn_decode_splits": (ctypes.c_int, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "slm_attn_version": (ctypes.c_char_p, []),
-    # slm_calib.h
-    "slm_calib_mfma_f32": (ctypes.c_int, [_I, _I, ctypes.POINTER(ctypes.c_double),
-                                          ctypes.POINTER(ctypes.c_double)]),
-    "slm_calib_hbm_read": (ctypes.c_int, [_I, ctypes.c_int64, _I,
-                                          ctypes.POINTER(ctypes.c_double)]),
     # slm_quant.h
     "slm_q4_matrix_create": (ctypes.c_int, [_I, ctypes.c_void_p, _I, _I, ctypes.POINTER(_P)]),
     "slm_q4_matrix_destroy": (None, [_P]),
@@ -723,17 +719,43 @@ def header_functions(*headers: os.PathLike | str) -> list[str]:
     """Names of the functions the given headers (default: every include/*.h) declare."""
     import re
 
-    paths = headers or (HEADER_PATH, CALIB_HEADER_PATH, QUANT_HEADER_PATH, LAYER_HEADER_PATH,
-                        GGUF_HEADER_PATH)
+    paths = headers or (HEADER_PATH, QUANT_HEADER_PATH, LAYER_HEADER_PATH, GGUF_HEADER_PATH)
     names = set()
     for h in paths:
         names |= set(re.findall(r"\b(slm_[a-z0-9_]+)\s*\(", Path(h).read_text()))
     return sorted(names)
 
 
+# the bench's measurement probes: libslm_calib.so, not part of the product
+CALIB_SIGNATURES = {
+    "slm_calib_mfma_f32": (ctypes.c_int, [_I, _I, ctypes.POINTER(ctypes.c_double),
+                                          ctypes.POINTER(ctypes.c_double)]),
+    "slm_calib_hbm_read": (ctypes.c_int, [_I, ctypes.c_int64, _I,
+                                          ctypes.POINTER(ctypes.c_double)]),
+}
+_calib_lib = None
+
+
+def load_calib_library() -> ctypes.CDLL:
+    """Loads calib/libslm_calib.so (the bench's probes); raises if not built."""
+    global _calib_lib
+    if _calib_lib is not None:
+        return _calib_lib
+    if not CALIB_LIB_PATH.exists():
+        raise FileNotFoundError(f"{CALIB_LIB_PATH} is missing: build the package first")
+    _share_torch_hip_runtime()
+    lib = ctypes.CDLL(str(CALIB_LIB_PATH))
+    for name, (res, args) in CALIB_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _calib_lib = lib
+    return lib
+
+
 def calibrate_mfma_f32(iters: int = 20000, device: int = 0) -> dict:
     """Measured v_mfma_f32_16x16x4_f32 rate of the device (slm_calib_mfma_f32)."""
-    lib = load_library()
+    lib = load_calib_library()
     tf, ms = ctypes.c_double(), ctypes.c_double()
     rc = lib.slm_calib_mfma_f32(device, iters, ctypes.byref(tf), ctypes.byref(ms))
     if rc != SLM_OK:
@@ -742,8 +764,9 @@ def calibrate_mfma_f32(iters: int = 20000, device: int = 0) -> dict:
 
 
 def calibrate_hbm_read(nbytes: int = 4 << 30, nontemporal: bool = True, device: int = 0) -> float:
-    """Measured streaming-read rate in GB/s (slm_calib_hbm_read)."""
-    lib = load_library()
+    """Rate of a plain streaming read in GB/s (slm_calib_hbm_read): a probe,
+    not a ceiling (the decode kernel streams faster at long context)."""
+    lib = load_calib_library()
     gbs = ctypes.c_double()
     rc = lib.slm_calib_hbm_read(device, nbytes, 1 if nontemporal else 0, ctypes.byref(gbs))
     if rc != SLM_OK:

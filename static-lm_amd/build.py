@@ -22,8 +22,10 @@ HOST_DEMO = PKG_DIR / "slm_host_demo"
 BUILD_DIR = PKG_DIR / "_build"
 
 HIP_SOURCES = ["slm_attn.hip", "slm_layer.hip", "slm_model.hip", "rope_append.hip",
-               "attn_decode.hip", "prefill_mfma.hip", "quant_gemm.hip", "norm_act.hip",
-               "calib.hip"]
+               "attn_decode.hip", "prefill_mfma.hip", "quant_gemm.hip", "norm_act.hip"]
+# measurement probes of the bench, a library of their own (not the product's)
+CALIB_DIR = PKG_DIR / "calib"
+CALIB_LIB = CALIB_DIR / "libslm_calib.so"
 # host-only C++ (no device code), compiled with the host compiler
 CPP_SOURCES = ["gguf.cpp"]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Werror",
@@ -79,6 +81,17 @@ def build_library(jobs: int = 4) -> Path:
     return LIB
 
 
+def build_calib() -> Path:
+    """The bench's measurement probes (calib/slm_calib.h) as libslm_calib.so."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    obj = BUILD_DIR / "calib.o"
+    _run([HIPCC, *HIP_FLAGS, f"-I{CALIB_DIR}", "-c", str(CALIB_DIR / "calib.hip"), "-o", str(obj)])
+    tmp = CALIB_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), str(obj)])
+    os.replace(tmp, CALIB_LIB)
+    return CALIB_LIB
+
+
 def build_host_demo() -> Path:
     """C++ host mirror of the reference interface, linked against the library."""
     _run([
@@ -92,6 +105,7 @@ def build_host_demo() -> Path:
 
 def build_all() -> None:
     build_library()
+    build_calib()
     build_host_demo()
 
 

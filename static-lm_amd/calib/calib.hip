@@ -6,7 +6,7 @@
 #include <stdint.h>
 #include <string.h>
 
-#include "../../include/slm_calib.h"
+#include "slm_calib.h"
 #include "attn_common.h"
 
 namespace {

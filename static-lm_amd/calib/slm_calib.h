@@ -1,19 +1,23 @@
 /*
- * slm_calib -- measurement helpers shipped in libslm_attn.so.
+ * slm_calib -- measurement probes for the bench (libslm_calib.so), kept out
+ * of the product library.
  *
- * No counterpart in static-lm: these time what one MI355X actually reaches on
- * the two resources the attention kernels are bound by, so a bench can report
- * measured ceilings next to the published peaks (8 TB/s HBM, 157.3 TFLOP/s
- * dense fp32 MFMA).  Both calls are synchronous, allocate and free their own
- * device memory and stream, and restore the caller's current device.
- * Return codes are those of slm_attn.h.
+ * No counterpart in static-lm.  slm_calib_mfma_f32 times the fp32 matrix
+ * cores with every SIMD busy; slm_calib_hbm_read times a plain streaming
+ * read.  Neither is a ceiling of the product kernels: the decode kernel at
+ * 131k positions streams faster than this read probe does.  The bench
+ * reports them next to the published peaks (8 TB/s HBM, 157.3 TFLOP/s dense
+ * fp32 MFMA), which remain the roofline denominators.  Both calls are
+ * synchronous, allocate and free their own device memory and stream, and
+ * restore the caller's current device.  Return codes are those of
+ * slm_attn.h.
  */
 #ifndef SLM_CALIB_H
 #define SLM_CALIB_H
 
 #include <stdint.h>
 
-#include "slm_attn.h"
+#include "../../include/slm_attn.h"
 
 #ifdef __cplusplus
 extern "C" {

@@ -24,6 +24,21 @@ def test_library_exports_every_header_function():
     assert set(declared) <= exported
 
 
+def test_measurement_probes_live_in_their_own_library():
+    # the bench's probes are libslm_calib.so, not exported by the product
+    declared = P.header_functions(P.CALIB_HEADER_PATH)
+    assert set(declared) == set(P.CALIB_SIGNATURES)
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(P.LIB_PATH)], capture_output=True,
+                        text=True, check=True).stdout
+    assert not any("slm_calib" in ln for ln in nm.splitlines())
+    cal = P.load_calib_library()
+    for name in declared:
+        assert hasattr(cal, name), name
+    # argument checks before any HIP call
+    assert cal.slm_calib_mfma_f32(0, 0, None, None) == P.ERR_ARG
+    assert cal.slm_calib_hbm_read(0, 1 << 20, 1, None) == P.ERR_ARG
+
+
 def test_version_and_null_handles():
     lib = P.load_library()
     assert b"gfx950" in lib.slm_attn_version()
@@ -33,9 +48,6 @@ def test_version_and_null_handles():
     assert lib.slm_kv_offset(None, 0, 0, 0) == ctypes.c_size_t(-1).value
     assert lib.slm_kv_device_ptr(None) is None
     lib.slm_attn_destroy(None)  # no-op
-    # measurement helpers check their arguments before any HIP call
-    assert lib.slm_calib_mfma_f32(0, 0, None, None) == P.ERR_ARG
-    assert lib.slm_calib_hbm_read(0, 1 << 20, 1, None) == P.ERR_ARG
     # quantized projections: argument checks before any device work
     out = P._P()
     assert lib.slm_q4_matrix_create(0, None, 4, 32, ctypes.byref(out)) == P.ERR_ARG
@@ -45,6 +57,7 @@ def test_version_and_null_handles():
     assert lib.slm_quantize_q8_0_dev(None, None, 32, None) == P.ERR_ARG
     assert lib.slm_gemm_q4_0_dev(None, None, None, 1, None) == P.ERR_ARG
     assert lib.slm_attn_decode_xb_dev(None, 0, 0, None, None, None, None, None) == P.ERR_ARG
+    assert lib.slm_attn_decode_xb_dev_noalloc(None, 0, 0, None, None, None, None, None) == P.ERR_ARG
     lib.slm_q4_matrix_destroy(None)  # no-op
 
 
