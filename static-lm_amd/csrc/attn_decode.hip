@@ -157,19 +157,37 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         }
     }
 
-    // q slice of each head: dims 4*(v*LPG + li) .. +3, rotated and pre-scaled.
-    // Every q and table load is issued before the first use: a load inside
-    // the rotate branch would wait for all earlier loads, the tile's included,
-    // once per slice.
+    // q of the GB heads, rotated at p and pre-scaled, is built once per
+    // workgroup in LDS: one float4 per thread of the first GB*HD/4.  (Loading
+    // each lane's own slice from memory replicated it 64*NW/LPG times per
+    // workgroup, ~80 KB of q and table traffic per CU for the Llama-3-8B
+    // shape, queued behind the first tile's loads: the second half of the
+    // waves got their first tile ~1 us after the first half.)  Every load is
+    // issued before the first use: a load inside the rotate branch would wait
+    // for all earlier loads, the tile's included.
     const bool rot = p.cos_t != nullptr;  // always set when appending
-    float4 qr[GB][NV];
-    float2 cr[NV], sr[NV];
-#pragma unroll
-    for (int i = 0; i < GB; ++i) {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) qr[i][v] = ld4(p.q + (h0 + i) * HD + 4 * (v * LPG + li));
+    constexpr int NQ4 = GB * HD / 4;
+    static_assert(NQ4 <= 64 * NW, "one q float4 per thread");
+    __shared__ __align__(16) float s_q[GB * HD];
+    if (threadIdx.x < NQ4) {
+        const int i = threadIdx.x / (HD / 4);
+        const int c = threadIdx.x - i * (HD / 4);
+        float4 x = ld4(p.q + (h0 + i) * HD + 4 * c);
+        float2 cq = make_float2(1.0f, 1.0f), sq = make_float2(0.0f, 0.0f);
+        if (rot) {
+            cq = *reinterpret_cast<const float2*>(p.cos_t + trow + 2 * c);
+            sq = *reinterpret_cast<const float2*>(p.sin_t + trow + 2 * c);
+        }
+        if (rot) x = rope4_exact(x, cq, sq);
+        x.x *= p.scale_log2;
+        x.y *= p.scale_log2;
+        x.z *= p.scale_log2;
+        x.w *= p.scale_log2;
+        *reinterpret_cast<float4*>(&s_q[i * HD + 4 * c]) = x;
     }
-    if (rot) {
+    // the owner's lanes rotate the appended k with their dims' table entries
+    float2 cr[NV], sr[NV];
+    if (append && owner) {
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const long j = trow + 2 * (v * LPG + li);
@@ -177,18 +195,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             sr[v] = *reinterpret_cast<const float2*>(p.sin_t + j);
         }
     }
+    __syncthreads();
+    float4 qr[GB][NV];
 #pragma unroll
     for (int i = 0; i < GB; ++i) {
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            float4 x = qr[i][v];
-            if (rot) x = rope4_exact(x, cr[v], sr[v]);
-            x.x *= p.scale_log2;
-            x.y *= p.scale_log2;
-            x.z *= p.scale_log2;
-            x.w *= p.scale_log2;
-            qr[i][v] = x;
-        }
+        for (int v = 0; v < NV; ++v)
+            qr[i][v] = *reinterpret_cast<const float4*>(&s_q[i * HD + 4 * (v * LPG + li)]);
     }
 
     float m[GB], l[GB];
