@@ -227,6 +227,19 @@ __device__ __forceinline__ float pair_sum(float a, float wa, float b, float wb) 
     return a * wa + b * wb;
 }
 
+// Max over the lane groups of a wave (lanes with equal index inside their
+// LPG-lane group); every lane gets the result.
+template <int LPG>
+__device__ __forceinline__ float groups_max(float x) {
+    if constexpr (LPG < 64) {
+        float a, b;
+        lane_pair<LPG>(x, a, b);
+        return groups_max<2 * LPG>(fmaxf(a, b));
+    } else {
+        return x;
+    }
+}
+
 // Merges the online-softmax states of lane groups OFF apart, then the next
 // level up to the whole wave.
 template <int OFF, int NV, int GB>

@@ -251,38 +251,63 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         if (tb != t0) load_tile(tb);
         attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
     }
-    merge_lane_groups<LPG, NV, GB>(m, l, o);
-
-    // merge the waves through LDS: this split's (max, sum, acc) per head
-    __shared__ __align__(16) float s_o[NW][GB][HD];
-    __shared__ float s_m[NW][GB];
-    __shared__ float s_l[NW][GB];
-    if (lg == 0) {
+    // Merge of the workgroup's NS lane-group states per head: the workgroup
+    // max M over the lane groups' maxima (max over the wave's lane groups by
+    // lane swaps, then over the waves through LDS), every lane group scales
+    // its (l, o) once by 2^(m - M) into its own LDS slot, and each thread sums
+    // the slots of one (head, dim) in slot order.  (Merging pairs of lane
+    // groups in registers first, with a scale per pair and round, cost ~360
+    // VALU ops per wave: ~1.5 us between a workgroup's last wave leaving the
+    // loop and the barrier, at two waves per SIMD.)
+    constexpr int NS = NW * GPW;  // lane-group states per workgroup
+    __shared__ float s_mw[NW][GB];
+    __shared__ __align__(16) float s_o[NS][GB][HD];
+    __shared__ float s_l[GB][NS];
+    float mg[GB];
 #pragma unroll
-        for (int i = 0; i < GB; ++i) {
+    for (int i = 0; i < GB; ++i) mg[i] = groups_max<LPG>(m[i]);
+    if (lane == 0) {
 #pragma unroll
-            for (int v = 0; v < NV; ++v)
-                *reinterpret_cast<float4*>(&s_o[wave][i][4 * (v * LPG + li)]) = o[i][v];
-            if (li == 0) {
-                s_m[wave][i] = m[i];
-                s_l[wave][i] = l[i];
-            }
+        for (int i = 0; i < GB; ++i) s_mw[wave][i] = mg[i];
+    }
+    __syncthreads();
+    float mwg[GB];  // the workgroup max per head, 0 when no position was seen
+#pragma unroll
+    for (int i = 0; i < GB; ++i) {
+        float mx = s_mw[0][i];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_mw[w][i]);
+        mwg[i] = mx;
+    }
+    const int slot = wave * GPW + lg;
+#pragma unroll
+    for (int i = 0; i < GB; ++i) {
+        const float mu = (mwg[i] == -INFINITY) ? 0.0f : mwg[i];
+        const float w = fast_exp2(m[i] - mu);  // 0 for a lane group that saw nothing
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            float4 x = o[i][v];
+            x.x *= w;
+            x.y *= w;
+            x.z *= w;
+            x.w *= w;
+            *reinterpret_cast<float4*>(&s_o[slot][i][4 * (v * LPG + li)]) = x;
         }
+        if (li == 0) s_l[i][slot] = l[i] * w;
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < GB * HD; idx += 64 * NW) {
         const int i = idx / HD;
         const int d = idx - i * HD;
-        float mx = s_m[0][i];
+        float mx = mwg[0];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_m[w][i]);
-        const float mu = (mx == -INFINITY) ? 0.0f : mx;
+        for (int j = 1; j < GB; ++j)
+            if (i == j) mx = mwg[j];
         float acc_o = 0.0f, acc_l = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float wt = fast_exp2(s_m[w][i] - mu);
-            acc_o += wt * s_o[w][i][d];
-            acc_l += wt * s_l[w][i];
+        for (int sl = 0; sl < NS; ++sl) {
+            acc_o += s_o[sl][i][d];
+            acc_l += s_l[i][sl];
         }
         const int h = h0 + i;
         if (p.n_splits == 1) {
