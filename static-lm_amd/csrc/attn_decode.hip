@@ -41,7 +41,6 @@ namespace slm {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxSplits = 1024;
 
 // Decode tiling per head_dim: lanes per position (LPG, 8 floats per lane
@@ -323,88 +322,66 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     }
 }
 
-// Head dims one combine workgroup merges: a divisor of head_dim, at most one
-// per lane (hd 96 takes three workgroups of 32).
+// Threads of a merge workgroup: one per head dim, rounded up to whole waves.
 template <int HD>
-constexpr int combine_width() {
-    return HD <= 64 ? HD : (HD % 64 == 0 ? 64 : 32);
+constexpr int combine_threads() {
+    return (HD + 63) / 64 * 64;
 }
+// Split partials a merge thread loads per round (all of them for up to 32
+// splits, which covers the split policy on 256 CUs).
+constexpr int kCombineRound = 32;
 
-// Log-sum-exp merge of the split partials: one workgroup per (head,
-// combine_width head dims).  The partial accumulators of a round of up to 64
-// splits are loaded before the split weights are known, so a round costs one
-// memory latency.
+// Log-sum-exp merge of the split partials: one workgroup per head, one
+// thread per head dim.  Every thread issues the loads of its dim's partials
+// first; wave 0 meanwhile turns the splits' (max, sum) pairs into weights
+// 2^(m_s - M) in LDS and the total sum; one barrier; each thread then sums
+// its dim over the splits in split order.  (Four waves splitting the splits
+// of a 64-dim slice, with a second barrier to add the waves' sums, cost
+// ~3 us per step at short contexts where an empty launch costs 2.4 us.)
 template <int HD>
-__global__ __launch_bounds__(kThreads) void decode_combine_kernel(DecodeParams p) {
-    constexpr int DW = combine_width<HD>();  // head dims per workgroup
-    static_assert(HD % DW == 0 && DW <= 64, "combine workgroups must tile head_dim");
-    constexpr int U = 16;                   // splits per wave per round
+__global__ __launch_bounds__(combine_threads<HD>()) void decode_combine_kernel(DecodeParams p) {
     __shared__ float s_w[kMaxSplits];
-    __shared__ float s_acc[kWaves][DW];
     __shared__ float s_ltot;
     const int h = blockIdx.x;
-    const int d = blockIdx.y * DW + (threadIdx.x & 63);
+    const int d = threadIdx.x;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
     const int ns = p.n_splits;
-    const float* src = p.part_o + (long)h * HD + (lane < DW ? d : 0);
+    const bool has_d = d < HD;
+    const float* src = p.part_o + (long)h * HD + (has_d ? d : 0);
     const long stride = (long)p.num_heads * HD;
 
-    // first round of accumulator loads, in flight while the weights are built
-    float x[U];
+    float x[kCombineRound];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int sp = wave + kWaves * u;
-        x[u] = sp < ns ? src[(long)sp * stride] : 0.0f;
-    }
-    if (wave == 0) {
+    for (int u = 0; u < kCombineRound; ++u) x[u] = u < ns ? src[(long)u * stride] : 0.0f;
+    if (threadIdx.x < 64) {
         const float2* ml = reinterpret_cast<const float2*>(p.part_ml);
-        constexpr int R = kMaxSplits / 64;
-        float2 v[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int sp = lane + 64 * r;
-            v[r] = sp < ns ? ml[(long)sp * p.num_heads + h] : make_float2(-INFINITY, 0.0f);
-        }
         float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < R; ++r) mx = fmaxf(mx, v[r].x);
+        for (int sp = lane; sp < ns; sp += 64) mx = fmaxf(mx, ml[(long)sp * p.num_heads + h].x);
         mx = wave_max(mx);
         float ls = 0.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int sp = lane + 64 * r;
-            if (sp < ns) {
-                const float w = fast_exp2(v[r].x - mx);
-                s_w[sp] = w;
-                ls += w * v[r].y;
-            }
+        for (int sp = lane; sp < ns; sp += 64) {
+            const float2 v = ml[(long)sp * p.num_heads + h];
+            const float w = fast_exp2(v.x - mx);
+            s_w[sp] = w;
+            ls += w * v.y;
         }
         ls = wave_sum(ls);
         if (lane == 0) s_ltot = ls;
     }
     __syncthreads();
     float acc = 0.0f;
-    for (int base = 0; base < ns; base += kWaves * U) {
-        if (base > 0) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int sp = base + wave + kWaves * u;
-                x[u] = sp < ns ? src[(long)sp * stride] : 0.0f;
-            }
-        }
+    for (int u = 0; u < kCombineRound; ++u)
+        if (u < ns) acc += s_w[u] * x[u];
+    for (int base = kCombineRound; base < ns; base += kCombineRound) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int sp = base + wave + kWaves * u;
-            if (sp < ns) acc += s_w[sp] * x[u];
-        }
+        for (int u = 0; u < kCombineRound; ++u)
+            x[u] = base + u < ns ? src[(long)(base + u) * stride] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kCombineRound; ++u)
+            if (base + u < ns) acc += s_w[base + u] * x[u];
     }
-    if (lane < DW) s_acc[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0 && lane < DW) {
-        const float tot = s_acc[0][lane] + s_acc[1][lane] + s_acc[2][lane] + s_acc[3][lane];
-        p.out[h * HD + d] = tot / s_ltot;
-    }
+    if (has_d) p.out[h * HD + d] = acc / s_ltot;
 }
 
 template <int HD, int GB>
@@ -423,13 +400,12 @@ hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st, hipE
 template <int HD>
 hipError_t launch_combine_t(const Shape& s, const DecodeParams& dp, hipStream_t st,
                             hipEvent_t ev0, hipEvent_t ev1) {
-    constexpr int DW = combine_width<HD>();
     if (ev0 != nullptr && ev1 != nullptr)
-        hipExtLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads, HD / DW),
-                              dim3(kThreads), 0, st, ev0, ev1, 0, dp);
+        hipExtLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads),
+                              dim3(combine_threads<HD>()), 0, st, ev0, ev1, 0, dp);
     else
-        hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads, HD / DW),
-                           dim3(kThreads), 0, st, dp);
+        hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads),
+                           dim3(combine_threads<HD>()), 0, st, dp);
     return hipGetLastError();
 }
 
