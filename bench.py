@@ -862,6 +862,9 @@ def main() -> int:
     ap.add_argument("--model-only", action="store_true",
                     help="only the whole model (prefill and greedy decode, Llama-3-8B shape); "
                          "prints its own JSON line, not the headline one")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="only the five workload configurations, GPU side (a short program for "
+                         "kernel traces); prints its own JSON line, not the headline one")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB: a plain "
                          "copy kernel of known size that scales rocprofv3 byte counters")
@@ -896,6 +899,11 @@ def main() -> int:
         log(f"copy calibration: {args.copy_calibration_mib} MiB read + "
             f"{args.copy_calibration_mib} MiB written")
         del src, dst
+
+    if args.configs_only:
+        wl, _ = bench_workloads(torch, P)
+        print(json.dumps({"configs": wl}))
+        return 0
 
     if args.layer_only:
         bl = bench_layer(torch, P, max(3, args.steps // 5))
