@@ -130,8 +130,10 @@ def fill_cache(torch, ctx, layers: int, msl: int, rows: int, seed: int) -> None:
     ctx.sync()
 
 
-def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
-    layers, ctx_len = 8, 32768
+def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768) -> dict:
+    """Decode at position ctx_len - 1 through 8 layers of the Llama-3-8B head
+    shape (KV caches of ctx_len rows each, rotated per step)."""
+    layers = 8
     pos = ctx_len - 1
     ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, ctx_len, layers, THETA)
     stream = torch.cuda.current_stream()
@@ -153,6 +155,12 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    # Two more untimed steps queued right before the timed ones: after the
+    # synchronize the GPU is idle and its clock takes a while to come back,
+    # which read ~3% slower over the 20 timed steps than steps that follow
+    # each other as in serving.
+    step()
+    step()
     e0.record(stream)
     for _ in range(steps):
         step()
@@ -162,6 +170,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int) -> dict:
     ms = e0.elapsed_time(e1)
 
     # second pass with per-launch events, for the dominant kernel's duration
+    step()
     ctx.profile(True)
     for _ in range(steps):
         step()
@@ -940,6 +949,18 @@ def main() -> int:
         log(f"prefill 4096: {pf['ms']:.3f} ms, {pf['tflops']:.2f} TFLOP/s")
         log("decode @131k")
         dl = bench_decode_131k(torch, P)
+        log("decode at short contexts")
+        short = {}
+        for n_ctx in (4096, 600):
+            ds = bench_decode_32k(torch, P, max(20, args.steps), args.warmup, ctx_len=n_ctx)
+            us = ds["ms"] / ds["steps"] / ds["layers"] * 1e3
+            short[f"ctx{n_ctx}"] = {
+                "us_per_layer_step": round(us, 3), "gbs": round(ds["gbs"], 1),
+                "frac_hbm": round(ds["gbs"] / HBM_PEAK_GBS, 4), "splits": ds["splits"],
+                "decode_kernel_us_stamped": round(ds["split_kernel_avg_us"], 3),
+                "combine_kernel_us_stamped": round(ds["combine_avg_us"], 3),
+            }
+            log(f"decode @{n_ctx}: {us:.2f} us per layer-step, {ds['gbs']:.0f} GB/s")
         log("all configurations")
         wl, wl_checks = bench_workloads(torch, P)
         log(f"decode @131k: {dl['ms_per_step']*1e3:.1f} us/step, {dl['gbs']:.1f} GB/s")
@@ -989,6 +1010,11 @@ def main() -> int:
                 "frac_fp32_mfma": pf["tflops"] / FP32_MFMA_PEAK_TFLOPS,
                 "kernel_avg_ms": pf["kernel_avg_ms"], "kernel_tflops": pf["kernel_tflops"],
                 "workload": "causal prefill 4096 tokens, 1 layer, start 0",
+            },
+            "decode_short": {
+                "workload": "decode at position ctx-1 through 8 layers of the Llama-3-8B head "
+                            "shape, steps back to back (decode + split merge per layer)",
+                **short,
             },
             "decode_131k": {
                 "gbs": dl["gbs"], "us_per_step": dl["ms_per_step"] * 1e3,
