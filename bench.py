@@ -67,17 +67,29 @@ def prefill_flops(start: int, n: int) -> int:
 TRAFFIC_PROFILE = REPO / "profiles" / "decode_kernel_llama3-8b_ctx32k_ctx131k.md"
 
 
+def _decode_profile_value(key: str) -> str | None:
+    try:
+        for ln in TRAFFIC_PROFILE.read_text().splitlines():
+            if ln.startswith(key + "(decode_kernel @ pos 32767):"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per launch of the 32k decode kernel from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy calibration),
     or None when the summary is absent."""
-    try:
-        for ln in TRAFFIC_PROFILE.read_text().splitlines():
-            if ln.startswith("traffic_bytes_per_launch(decode_kernel @ pos 32767):"):
-                return int(ln.split(":", 1)[1])
-    except OSError:
-        pass
-    return None
+    v = _decode_profile_value("traffic_bytes_per_launch")
+    return int(v) if v else None
+
+
+def trace_mean_us() -> float | None:
+    """Mean duration of the 32k decode launches in the committed rocprofv3
+    kernel-trace summary, or None when it is absent."""
+    v = _decode_profile_value("trace_mean_us")
+    return float(v) if v else None
 
 
 PREFILL_PROFILE = REPO / "profiles" / "prefill_mfma_kernel_llama3-8b_4096.md"
@@ -200,6 +212,24 @@ def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768) ->
         "combine_avg_us": comb_ms / max(n_comb, 1) * 1e3,
         "_check": check,
     }
+
+
+def bench_decode_short(torch, P, args) -> dict:
+    """Decode steps back to back at 4096 and 600 cached rows (8 layers of the
+    Llama-3-8B head shape): the latency-bound lengths of the C4 decode steps
+    and of a model decode after a 512-token prompt."""
+    short = {}
+    for n_ctx in (4096, 600):
+        ds = bench_decode_32k(torch, P, max(20, args.steps), args.warmup, ctx_len=n_ctx)
+        us = ds["ms"] / ds["steps"] / ds["layers"] * 1e3
+        short[f"ctx{n_ctx}"] = {
+            "us_per_layer_step": round(us, 3), "gbs": round(ds["gbs"], 1),
+            "frac_hbm": round(ds["gbs"] / HBM_PEAK_GBS, 4), "splits": ds["splits"],
+            "decode_kernel_us_stamped": round(ds["split_kernel_avg_us"], 3),
+            "combine_kernel_us_stamped": round(ds["combine_avg_us"], 3),
+        }
+        log(f"decode @{n_ctx}: {us:.2f} us per layer-step, {ds['gbs']:.0f} GB/s")
+    return short
 
 
 def bench_prefill_4k(torch, P, reps: int) -> dict:
@@ -871,6 +901,10 @@ def main() -> int:
     ap.add_argument("--model-only", action="store_true",
                     help="only the whole model (prefill and greedy decode, Llama-3-8B shape); "
                          "prints its own JSON line, not the headline one")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode measurements (8 layers at 32767, 131072..131135, 8 layers "
+                         "at 4095 and at 599; a short program for kernel traces); prints its own "
+                         "JSON line, not the headline one")
     ap.add_argument("--configs-only", action="store_true",
                     help="only the five workload configurations, GPU side (a short program for "
                          "kernel traces); prints its own JSON line, not the headline one")
@@ -938,6 +972,15 @@ def main() -> int:
                           "kernel_avg_ms": pf["kernel_avg_ms"]}))
         return 0
 
+    if args.decode_only:
+        d = bench_decode_32k(torch, P, args.steps, args.warmup)
+        dl = bench_decode_131k(torch, P)
+        short = bench_decode_short(torch, P, args)
+        print(json.dumps({"decode_32k_us_per_layer_step": d["ms"] / d["steps"] / d["layers"] * 1e3,
+                          "decode_32k_gbs": d["gbs"], "decode_131k_us_per_step": dl["ms_per_step"] * 1e3,
+                          "decode_short": short}))
+        return 0
+
     log("decode @32k")
     d = bench_decode_32k(torch, P, args.steps, args.warmup)
     log(f"decode @32k: {d['gbs']:.1f} GB/s, split kernel {d['split_kernel_avg_us']:.1f} us "
@@ -950,17 +993,7 @@ def main() -> int:
         log("decode @131k")
         dl = bench_decode_131k(torch, P)
         log("decode at short contexts")
-        short = {}
-        for n_ctx in (4096, 600):
-            ds = bench_decode_32k(torch, P, max(20, args.steps), args.warmup, ctx_len=n_ctx)
-            us = ds["ms"] / ds["steps"] / ds["layers"] * 1e3
-            short[f"ctx{n_ctx}"] = {
-                "us_per_layer_step": round(us, 3), "gbs": round(ds["gbs"], 1),
-                "frac_hbm": round(ds["gbs"] / HBM_PEAK_GBS, 4), "splits": ds["splits"],
-                "decode_kernel_us_stamped": round(ds["split_kernel_avg_us"], 3),
-                "combine_kernel_us_stamped": round(ds["combine_avg_us"], 3),
-            }
-            log(f"decode @{n_ctx}: {us:.2f} us per layer-step, {ds['gbs']:.0f} GB/s")
+        short = bench_decode_short(torch, P, args)
         log("all configurations")
         wl, wl_checks = bench_workloads(torch, P)
         log(f"decode @131k: {dl['ms_per_step']*1e3:.1f} us/step, {dl['gbs']:.1f} GB/s")
@@ -1040,6 +1073,7 @@ def main() -> int:
                     f"max-abs {c['parity']['max_abs']:.2e}, KV bitwise {c['parity']['kv_bitwise']}")
 
     ms_per_step = d["ms"] / d["steps"]
+    tmu = trace_mean_us()
     res = {
         "metric": METRIC,
         "value": round(d["gbs"], 2),
@@ -1073,6 +1107,11 @@ def main() -> int:
             "avg_launch_us": round(d["split_kernel_avg_us"], 3),
             "combine_kernel_avg_us": round(d["combine_avg_us"], 3),
             "algorithmic_bytes_per_launch": d["split_kernel_bytes"],
+            # the same kernel's mean over the committed kernel trace, and the
+            # fraction it gives (the launch-stamped events above read ~1.5% lower)
+            "trace_mean_us": tmu,
+            "trace_frac": (round(d["split_kernel_bytes"] / (tmu * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                           if tmu else None),
         },
         "cpu_baseline": cpu,
         "parity": cpu["parity"] if cpu else None,
