@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from oracle import py_oracle as orc
-from slm_testlib import (WORKLOADS, assert_bitwise, assert_close, gen, layer_inputs,
+from slm_testlib import (WORKLOADS, Workload, assert_bitwise, assert_close, gen, layer_inputs,
                          load_product, prefilled_rows)
 
 P = load_product()
@@ -238,6 +238,41 @@ def test_device_entry_points_match_oracle():
         s.synchronize()
         ctx.set_stream(None)
         assert_close(o.cpu().numpy(), om.decode(1, n, q2, k2, v2), what="decode_dev")
+
+
+@pytest.mark.parametrize("shape,positions", [
+    ((256, 4, 4, 512), (0, 7, 300, 511)),          # C1's head shape (MHA, hd 64)
+    ((576, 9, 3, 1024), (0, 33, 257, 1000)),       # SmolLM2-135M (GQA kv_mul 3, hd 64)
+    ((4096, 32, 8, 1200), (0, 255, 256, 1199)),    # Llama-3-8B (GQA kv_mul 4, hd 128): 1 and 9+ splits
+])
+def test_attend_against_scalar_attention(shape, positions):
+    """The device attention against causal_multi_head_attention, the
+    reference's scalar path (transformer.rs:214-271: sequential max, libm
+    expf, sequential sum), directly rather than through the JIT restatement:
+    the reference holds its layer outputs to 1e-4 of that path
+    (transformer.rs:1000-1099), and so does this test."""
+    torch = pytest.importorskip("torch")
+    dim, heads, kvh, msl = shape
+    w = Workload("scalar-check", dim, heads, kvh, msl, 1, 1e4, 0, 0, seed=0x5EED0020 + dim)
+    cfg = w.cfg()
+    rows = max(positions) + 1
+    kc = np.zeros((msl, w.kv_dim), np.float32)
+    vc = np.zeros((msl, w.kv_dim), np.float32)
+    kc[:rows] = prefilled_rows(w, 0, 0, 0, rows)
+    vc[:rows] = prefilled_rows(w, 0, 1, 0, rows)
+    with make_ctx(w) as ctx:
+        ctx.kv_write(0, 0, 0, kc[:rows])
+        ctx.kv_write(0, 1, 0, vc[:rows])
+        for pos in positions:
+            q = gen([w.seed, 7, pos], dim)
+            qd = torch.from_numpy(q).cuda()
+            out = torch.empty(dim, device="cuda")
+            ctx.attend_dev(0, pos, qd.data_ptr(), out.data_ptr())
+            ctx.sync()
+            ref = orc.attention(q, kc, vc, cfg, pos, jit=False)
+            ns, _ = ctx.decode_splits(pos + 1)
+            log(f"{shape} pos {pos} ({ns} splits): vs scalar attention")
+            assert_close(out.cpu().numpy(), ref, what=f"attend_dev vs scalar pos {pos}")
 
 
 def test_error_codes_mirror_reference_asserts():
