@@ -640,7 +640,8 @@ def prefilled_cache(ci: int, rows: int, kvd: int):
 def bench_workloads(torch, P) -> tuple[list, list]:
     """Each configuration end to end on device pointers: per layer one prefill
     of P rows then D decode steps.  Reports the host-bound wall time of a pass
-    (one Python call per launch) next to the kernels' own time (launch-stamped
+    (one Python call per launch), the time of the same pass replayed as a HIP
+    graph (one host call), and the kernels' own time (launch-stamped
     decode and merge events, events around the other launches), with the
     algorithmic rates and roofline fractions of the prefill and decode kernels.
     Also returns, per configuration, the inputs, outputs and appended cache
@@ -680,6 +681,19 @@ def bench_workloads(torch, P) -> tuple[list, list]:
         e1.record(stream)
         torch.cuda.synchronize()
         wall_ms = e0.elapsed_time(e1)
+        # the same pass recorded once as a HIP graph and replayed with one
+        # host call: the dispatch cost without the per-call host round trip
+        ctx.capture_begin()
+        run()
+        graph = ctx.capture_end()
+        ctx.graph_launch(graph)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        ctx.graph_launch(graph)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        graph_ms = e0.elapsed_time(e1)
+        graph.close()
         ctx.profile(True)
         run()
         prof = ctx.profile_read()
@@ -690,7 +704,7 @@ def bench_workloads(torch, P) -> tuple[list, list]:
         kern = {kind: round(ms, 4) for kind, (cnt, ms) in prof.items() if cnt}
         pf_ms = prof["prefill"][1] + prof["append"][1]
         dec_ms = prof["decode"][1] + prof["combine"][1]
-        rec = {"workload": name, "wall_ms": round(wall_ms, 4),
+        rec = {"workload": name, "wall_ms": round(wall_ms, 4), "graph_ms": round(graph_ms, 4),
                "kernel_ms": round(sum(ms for _, ms in prof.values()), 4),
                "kernel_ms_by_kind": kern,
                "launches": int(sum(cnt for cnt, _ in prof.values())),
@@ -702,7 +716,10 @@ def bench_workloads(torch, P) -> tuple[list, list]:
         rec["decode_gbs"] = round(dec_bytes / (dec_ms / 1e3) / 1e9, 1)
         rec["decode_frac_hbm"] = round(dec_bytes / (dec_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
         rec["kernel_frac_of_wall"] = round(rec["kernel_ms"] / wall_ms, 3)
+        rec["kernel_frac_of_graph"] = round(rec["kernel_ms"] / graph_ms, 3)
         out.append(rec)
+        log(f"{name}: wall {wall_ms:.3f} ms per pass, graph replay {graph_ms:.3f} ms, "
+            f"kernels {rec['kernel_ms']:.3f} ms over {rec['launches']} launches")
         got = o.cpu().numpy()
         kv_rows = [(ctx.kv_read(l, 0, pre, rows), ctx.kv_read(l, 1, pre, rows))
                    for l in range(layers)]

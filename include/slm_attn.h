@@ -63,6 +63,10 @@ extern "C" {
 #define SLM_ERR_UNSUPPORTED (-8)
 /* No gfx950 device, or the library's device code cannot run on it. */
 #define SLM_ERR_DEVICE (-9)
+/* The call cannot be recorded into a graph (it synchronizes, copies host
+ * memory or would allocate) and the context's stream is being captured; or a
+ * capture call out of order (slm_attn_capture_begin). */
+#define SLM_ERR_CAPTURE (-23)
 
 /* TransformerConfig fields that attention uses (transformer.rs:8-33) plus
  * the layer count and RoPE base.  The reference hard-codes the base to
@@ -145,6 +149,26 @@ int slm_attn_set_stream(slm_attn_ctx* ctx, void* stream);
 void* slm_attn_get_stream(const slm_attn_ctx* ctx);
 /* Wait for all work enqueued on the context stream. */
 int slm_attn_sync(slm_attn_ctx* ctx);
+
+/* ---- HIP graphs ------------------------------------------------------------
+ * No counterpart in the reference (its calls run on CPU threads).  For callers
+ * that replay a fixed sequence of device-pointer calls (a serving loop, a
+ * benchmark pass): between slm_attn_capture_begin and slm_attn_capture_end the
+ * context's stream is captured (HIP stream capture, this thread only), so the
+ * device-pointer entry points record their kernels instead of running them;
+ * slm_attn_graph_launch replays the recording on the context's stream with one
+ * host call.  A replay repeats the recorded arguments (positions, pointers):
+ * the caller changes inputs in the device buffers between replays.  While
+ * capturing, calls that synchronize, copy host memory, change the stream,
+ * time kernels or would grow a workspace return SLM_ERR_CAPTURE and record
+ * nothing (make one uncaptured call first to size workspaces).  Captured
+ * launches carry no memset nodes.  Other work on the same stream during the
+ * capture (from other libraries) is recorded too. */
+typedef struct slm_attn_graph slm_attn_graph;
+int slm_attn_capture_begin(slm_attn_ctx* ctx);
+int slm_attn_capture_end(slm_attn_ctx* ctx, slm_attn_graph** out);
+int slm_attn_graph_launch(slm_attn_ctx* ctx, const slm_attn_graph* graph);
+void slm_attn_graph_destroy(slm_attn_graph* graph);
 
 /* ---- raw KV cache access (pre-fill, snapshot/restore, bit-exact checks) ---
  * which: 0 = K, 1 = V.  Rows pos0..pos0+n-1, each kv_dim floats.  Host

@@ -54,11 +54,13 @@ ERRORS = {
     -20: "SLM_ERR_TYPE",
     -21: "SLM_ERR_BOUNDS",
     -22: "SLM_ERR_UNALIGNED",
+    -23: "SLM_ERR_CAPTURE",
 }
 (ERR_CONFIG, ERR_POS, ERR_BATCH, ERR_LAYER, ERR_ALIAS, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED,
  ERR_DEVICE, ERR_SHAPE, ERR_TOKEN) = (-1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11)
 (ERR_IO, ERR_EOF, ERR_MAGIC, ERR_VERSION, ERR_UTF8, ERR_VALUE_TYPE, ERR_DIMS, ERR_NOT_FOUND,
  ERR_TYPE, ERR_BOUNDS, ERR_UNALIGNED) = tuple(range(-12, -23, -1))
+ERR_CAPTURE = -23
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8
 
 KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope", "quant", "gemm", "norm",
@@ -130,6 +132,10 @@ SIGNATURES = {
     "slm_attn_set_stream": (ctypes.c_int, [_P, _P]),
     "slm_attn_get_stream": (_P, [_P]),
     "slm_attn_sync": (ctypes.c_int, [_P]),
+    "slm_attn_capture_begin": (ctypes.c_int, [_P]),
+    "slm_attn_capture_end": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
+    "slm_attn_graph_launch": (ctypes.c_int, [_P, _P]),
+    "slm_attn_graph_destroy": (None, [_P]),
     "slm_kv_write": (ctypes.c_int, [_P, _I, _I, _I, _I, _F]),
     "slm_kv_read": (ctypes.c_int, [_P, _I, _I, _I, _I, _F]),
     "slm_kv_write_dev": (ctypes.c_int, [_P, _I, _I, _I, _I, _P]),
@@ -459,6 +465,20 @@ class AttentionContext:
     def sync(self) -> None:
         self._check(self.lib.slm_attn_sync(self._h))
 
+    # -- HIP graphs -------------------------------------------------------------
+    def capture_begin(self) -> None:
+        """Device-pointer calls from here to capture_end() are recorded, not run."""
+        self._check(self.lib.slm_attn_capture_begin(self._h))
+
+    def capture_end(self) -> "AttentionGraph":
+        g = _P()
+        self._check(self.lib.slm_attn_capture_end(self._h, ctypes.byref(g)))
+        return AttentionGraph(self.lib, g)
+
+    def graph_launch(self, graph: "AttentionGraph") -> None:
+        """Replays a recording on the context stream (asynchronous)."""
+        self._check(self.lib.slm_attn_graph_launch(self._h, graph.handle))
+
     def kv_write(self, layer: int, which: int, pos0: int, rows) -> None:
         rows = np.ascontiguousarray(rows, dtype=np.float32).reshape(-1, self.cfg.kv_dim())
         self._check(self.lib.slm_kv_write(self._h, layer, which, pos0, rows.shape[0], _fptr(rows)))
@@ -499,6 +519,35 @@ class AttentionContext:
         self._check(self.lib.slm_attn_decode_splits(self._h, seq_len, ctypes.byref(ns),
                                                     ctypes.byref(tile)))
         return ns.value, tile.value
+
+
+class AttentionGraph:
+    """A recording of device-pointer calls (slm_attn_capture_end)."""
+
+    def __init__(self, lib, handle):
+        self.lib = lib
+        self._h = handle
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.slm_attn_graph_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Q4Matrix:

@@ -65,6 +65,12 @@ int hip_fail(slm_attn_ctx* c, hipError_t e, const char* what) {
                 std::string(what) + ": " + hipGetErrorString(e));
 }
 
+int refuse_capture(slm_attn_ctx* c, const char* what) {
+    return fail(c, SLM_ERR_CAPTURE,
+                std::string(what) +
+                    ": not allowed while the context's stream is being captured into a graph");
+}
+
 
 // LayerWorkspace::allocate asserts (transformer.rs:81-101).
 int validate(const slm_attn_config* cfg, std::string* why) {
@@ -308,6 +314,7 @@ int do_attend(slm_attn_ctx* c, int layer, int start, int n, const float* q,
 
 int ensure_stage(slm_attn_ctx* c, size_t floats) {
     if (c->stage_floats >= floats) return SLM_OK;
+    if (c->capturing) return refuse_capture(c, "host staging buffer");
     if (c->stage) {
         SLM_HIP(c, hipStreamSynchronize(c->stream));
         SLM_HIP(c, hipFree(c->stage));
@@ -568,6 +575,11 @@ int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
 void slm_attn_destroy(slm_attn_ctx* c) {
     if (!c) return;
     // Teardown is best effort: errors here have no caller to report to.
+    if (c->capturing) {  // an unfinished capture is dropped
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(c->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        c->capturing = false;
+    }
     if (c->own_stream) (void)hipStreamSynchronize(c->own_stream);
     if (c->stream && c->stream != c->own_stream)
         (void)hipStreamSynchronize(c->stream);
@@ -606,6 +618,7 @@ void slm_attn_destroy(slm_attn_ctx* c) {
 
 int slm_attn_set_stream(slm_attn_ctx* c, void* stream) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_attn_set_stream");
     c->stream = stream ? (hipStream_t)stream : c->own_stream;
     return SLM_OK;
 }
@@ -616,8 +629,61 @@ void* slm_attn_get_stream(const slm_attn_ctx* c) {
 
 int slm_attn_sync(slm_attn_ctx* c) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_attn_sync");
     SLM_HIP(c, hipStreamSynchronize(c->stream));
     return SLM_OK;
+}
+
+int slm_attn_capture_begin(slm_attn_ctx* c) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return fail(c, SLM_ERR_CAPTURE, "a capture is already in progress");
+    if (c->profiling)
+        return fail(c, SLM_ERR_CAPTURE, "kernel timing must be off while capturing");
+    SLM_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+    return SLM_OK;
+}
+
+int slm_attn_capture_end(slm_attn_ctx* c, slm_attn_graph** out) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (out) *out = nullptr;
+    if (!c->capturing) return fail(c, SLM_ERR_CAPTURE, "no capture in progress");
+    c->capturing = false;  // the stream leaves capture mode whatever follows
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return hip_fail(c, e, "hipStreamEndCapture");
+    }
+    if (!out) {
+        (void)hipGraphDestroy(g);
+        return fail(c, SLM_ERR_ARG, "out is NULL (the capture was dropped)");
+    }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_fail(c, e, "hipGraphInstantiate");
+    }
+    *out = new slm_attn_graph{c->device, g, x};
+    return SLM_OK;
+}
+
+int slm_attn_graph_launch(slm_attn_ctx* c, const slm_attn_graph* g) {
+    if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_attn_graph_launch");
+    if (!g) return fail(c, SLM_ERR_ARG, "graph is NULL");
+    if (g->device != c->device)
+        return fail(c, SLM_ERR_DEVICE, "the graph was captured on another device");
+    SLM_HIP(c, hipGraphLaunch(g->exec, c->stream));
+    return SLM_OK;
+}
+
+void slm_attn_graph_destroy(slm_attn_graph* g) {
+    if (!g) return;
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+    delete g;
 }
 
 int slm_kv_append_dev(slm_attn_ctx* c, int32_t layer, int32_t pos0, int32_t n,
@@ -707,6 +773,7 @@ int slm_attn_prefill_dev(slm_attn_ctx* c, int32_t layer, int32_t start,
 int slm_attn_decode(slm_attn_ctx* c, int32_t layer, int32_t pos, const float* q,
                     const float* k, const float* v, float* out) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_attn_decode");
     int rc;
     // the decode asserts, in the reference's order (transformer.rs:404-407)
     if ((rc = check_layer(c, layer)) || (rc = check_pos(c, pos))) return rc;
@@ -717,6 +784,7 @@ int slm_attn_prefill(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t n,
                      const float* q, const float* k, const float* v,
                      float* out) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_attn_prefill");
     const slm::Shape& s = c->shape;
     int rc;
     if ((rc = check_layer(c, layer)) || (rc = check_batch(c, start, n)))
@@ -749,6 +817,7 @@ int slm_attn_prefill(slm_attn_ctx* c, int32_t layer, int32_t start, int32_t n,
 int slm_kv_write(slm_attn_ctx* c, int32_t layer, int32_t which, int32_t pos0,
                  int32_t n, const float* rows) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_kv_write");
     int rc;
     if ((rc = check_layer(c, layer))) return rc;
     if (which != 0 && which != 1) return fail(c, SLM_ERR_ARG, "which must be 0 or 1");
@@ -782,6 +851,7 @@ int slm_kv_write_dev(slm_attn_ctx* c, int32_t layer, int32_t which,
 int slm_kv_read(slm_attn_ctx* c, int32_t layer, int32_t which, int32_t pos0,
                 int32_t n, float* rows) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_kv_read");
     int rc;
     if ((rc = check_layer(c, layer))) return rc;
     if (which != 0 && which != 1) return fail(c, SLM_ERR_ARG, "which must be 0 or 1");
@@ -808,6 +878,7 @@ float* slm_kv_device_ptr(const slm_attn_ctx* c) { return c ? c->kv : nullptr; }
 
 int slm_rope_tables_read(slm_attn_ctx* c, float* cos_out, float* sin_out) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_rope_tables_read");
     if (!cos_out || !sin_out) return fail(c, SLM_ERR_ARG, "NULL buffer");
     const size_t bytes = (size_t)c->cfg.max_seq_len * c->shape.half * 4;
     SLM_HIP(c, hipMemcpyAsync(cos_out, c->cos_t, bytes, hipMemcpyDeviceToHost,
@@ -820,12 +891,14 @@ int slm_rope_tables_read(slm_attn_ctx* c, float* cos_out, float* sin_out) {
 
 int slm_attn_profile(slm_attn_ctx* c, int32_t enable) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_attn_profile");
     c->profiling = enable != 0;
     return SLM_OK;
 }
 
 int slm_attn_profile_read(slm_attn_ctx* c, slm_kernel_stat* out) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_attn_profile_read");
     if (!out) return fail(c, SLM_ERR_ARG, "NULL buffer");
     SLM_HIP(c, hipStreamSynchronize(c->stream));
     for (auto& p : c->pending) {

@@ -85,6 +85,8 @@ struct slm_attn_ctx {
     size_t mdl_parts_n = 0;
     int32_t* tok_pin = nullptr;            // pinned [2]: generate's tokens, read back
     hipEvent_t tok_ev[2] = {nullptr, nullptr};  // one step behind the device
+    // the stream is being captured into a HIP graph (slm_attn_capture_begin)
+    bool capturing = false;
     // kernel timing
     bool profiling = false;
     struct Pending {
@@ -98,10 +100,20 @@ struct slm_attn_ctx {
     std::string err;
 };
 
+// A captured sequence of launches (slm_attn_capture_end), replayed on a
+// context's stream by slm_attn_graph_launch.
+struct slm_attn_graph {
+    int device;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
 namespace slm_host {
 
 int fail(slm_attn_ctx* c, int code, const std::string& msg);
 int hip_fail(slm_attn_ctx* c, hipError_t e, const char* what);
+// SLM_ERR_CAPTURE for a call that cannot be recorded into a graph
+int refuse_capture(slm_attn_ctx* c, const char* what);
 
 #define SLM_HIP(c, expr)                                   \
     do {                                                   \
@@ -164,6 +176,7 @@ struct Timed {
 template <class T>
 int ensure_buffer(slm_attn_ctx* c, T** buf, size_t* have, size_t want, const char* what) {
     if (*have >= want) return SLM_OK;
+    if (c->capturing) return refuse_capture(c, what);
     if (*buf) {
         SLM_HIP(c, hipStreamSynchronize(c->stream));
         SLM_HIP(c, hipFree(*buf));

@@ -400,6 +400,7 @@ extern "C" {
 int slm_model_forward_token_dev(slm_attn_ctx* c, const slm_model_weights* w, float rms_eps,
                                 int32_t token, int32_t pos, float* logits, int32_t* next_token) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_model_forward_token_dev");
     int rc;
     if ((rc = check_pos(c, pos))) return rc;
     return model_prefill(c, w, rms_eps, &token, 1, pos, logits, next_token);
@@ -409,6 +410,7 @@ int slm_model_prefill_dev(slm_attn_ctx* c, const slm_model_weights* w, float rms
                           const int32_t* tokens, int32_t n, int32_t start, float* logits,
                           int32_t* next_token) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_model_prefill_dev");
     return model_prefill(c, w, rms_eps, tokens, n, start, logits, next_token);
 }
 
@@ -416,6 +418,7 @@ int slm_model_generate_dev(slm_attn_ctx* c, const slm_model_weights* w, float rm
                            const int32_t* prompt, int32_t n_prompt, int32_t* out_tokens,
                            int32_t max_out, int32_t eos, int32_t* n_out) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_model_generate_dev");
     if (!n_out) return fail(c, SLM_ERR_ARG, "n_out is NULL");
     *n_out = 0;
     if (max_out <= 0 || n_prompt <= 0) return SLM_OK;  // transformer.rs:862-864
@@ -458,6 +461,7 @@ int slm_model_generate_dev(slm_attn_ctx* c, const slm_model_weights* w, float rm
 int slm_model_embed_dev(slm_attn_ctx* c, const slm_model_weights* w, float rms_eps,
                         const int32_t* tokens, int32_t n, float* out) {
     if (!c) return fail(nullptr, SLM_ERR_ARG, "ctx is NULL");
+    if (c->capturing) return refuse_capture(c, "slm_model_embed_dev");
     const slm::Shape& s = c->shape;
     int rc, vocab = 0;
     if ((rc = check_model(c, w, &vocab)) || (rc = check_batch(c, 0, n)) ||
