@@ -12,6 +12,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <new>
 #include <string>
 #include <unordered_map>
 
@@ -241,7 +242,11 @@ int slm_gguf_open(const char* path, slm_gguf** out) {
         base = static_cast<const uint8_t*>(m);
     }
     close(fd);
-    slm_gguf* g = new slm_gguf();
+    slm_gguf* g = new (std::nothrow) slm_gguf();
+    if (!g) {
+        if (size) munmap(const_cast<uint8_t*>(base), size);
+        return fail(SLM_ERR_IO, "Io: out of host memory for the file handle");
+    }
     g->base = base;
     g->size = size;
     auto bail = [&](int code, const std::string& msg) {

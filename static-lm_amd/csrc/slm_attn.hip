@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -508,7 +509,8 @@ int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
                     std::string("device is ") + prop.gcnArchName +
                         ", this library is built for gfx950 only");
 
-    slm_attn_ctx* c = new slm_attn_ctx();
+    slm_attn_ctx* c = new (std::nothrow) slm_attn_ctx();
+    if (!c) return fail(nullptr, SLM_ERR_HIP, "out of host memory for the context");
     c->cfg = *cfg;
     c->device = dev;
     slm::Shape& s = c->shape;
@@ -665,7 +667,13 @@ int slm_attn_capture_end(slm_attn_ctx* c, slm_attn_graph** out) {
         (void)hipGraphDestroy(g);
         return hip_fail(c, e, "hipGraphInstantiate");
     }
-    *out = new slm_attn_graph{c->device, g, x};
+    slm_attn_graph* r = new (std::nothrow) slm_attn_graph{c->device, g, x};
+    if (!r) {
+        (void)hipGraphExecDestroy(x);
+        (void)hipGraphDestroy(g);
+        return fail(c, SLM_ERR_HIP, "out of host memory for the graph handle");
+    }
+    *out = r;
     return SLM_OK;
 }
 
@@ -962,7 +970,8 @@ int slm_q4_matrix_create(int32_t device, const void* blocks, int32_t rows, int32
     }
     int prev = 0;
     if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-    slm_q4_matrix* m = new slm_q4_matrix();
+    slm_q4_matrix* m = new (std::nothrow) slm_q4_matrix();
+    if (!m) return fail(nullptr, SLM_ERR_HIP, "out of host memory for the matrix handle");
     m->device = device;
     m->rows = rows;
     m->cols = cols;

@@ -4,6 +4,7 @@
 // slm_model_*_dev entry points take.
 #include "../../include/slm_gguf.h"
 
+#include <new>
 #include <string>
 #include <vector>
 
@@ -131,7 +132,8 @@ int slm_model_load_gguf(const slm_gguf* g, int32_t device, int32_t num_layers,
     if (dim == 0 || dim % 32 != 0)
         return fail(nullptr, SLM_ERR_SHAPE, "token_embd.weight rows must be a multiple of 32 long");
     if ((rc = check_model_file(g, num_layers, dim))) return rc;
-    slm_model* m = new slm_model();
+    slm_model* m = new (std::nothrow) slm_model();
+    if (!m) return fail(nullptr, SLM_ERR_HIP, "out of host memory for the model handle");
     m->device = device;
     auto bail = [&](int code) {
         slm_model_destroy(m);

@@ -48,6 +48,11 @@ def test_version_and_null_handles():
     assert lib.slm_kv_offset(None, 0, 0, 0) == ctypes.c_size_t(-1).value
     assert lib.slm_kv_device_ptr(None) is None
     lib.slm_attn_destroy(None)  # no-op
+    g = ctypes.c_void_p(1)
+    assert lib.slm_attn_capture_begin(None) == P.ERR_ARG
+    assert lib.slm_attn_capture_end(None, ctypes.byref(g)) == P.ERR_ARG
+    assert lib.slm_attn_graph_launch(None, None) == P.ERR_ARG
+    lib.slm_attn_graph_destroy(None)  # no-op
     # quantized projections: argument checks before any device work
     out = P._P()
     assert lib.slm_q4_matrix_create(0, None, 4, 32, ctypes.byref(out)) == P.ERR_ARG
