@@ -994,7 +994,10 @@ def main() -> int:
         dl = bench_decode_131k(torch, P)
         short = bench_decode_short(torch, P, args)
         print(json.dumps({"decode_32k_us_per_layer_step": d["ms"] / d["steps"] / d["layers"] * 1e3,
-                          "decode_32k_gbs": d["gbs"], "decode_131k_us_per_step": dl["ms_per_step"] * 1e3,
+                          "decode_32k_gbs": d["gbs"],
+                          "decode_32k_kernel_us_stamped": d["split_kernel_avg_us"],
+                          "decode_32k_combine_us_stamped": d["combine_avg_us"],
+                          "decode_131k_us_per_step": dl["ms_per_step"] * 1e3,
                           "decode_short": short}))
         return 0
 
