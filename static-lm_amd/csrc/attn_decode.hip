@@ -350,16 +350,28 @@ __global__ __launch_bounds__(combine_threads<HD>()) void decode_combine_kernel(D
     const float* src = p.part_o + (long)h * HD + (has_d ? d : 0);
     const long stride = (long)p.num_heads * HD;
 
+    // the (max, sum) pairs of the first 64 splits go out before the
+    // partials: loads complete in issue order, so wave 0 forms the weights
+    // while the partials are still in flight.  Every load is unconditional
+    // (indices clamped, values past ns never used), so the compiler can
+    // count them and wait for the pairs alone.
+    const float2* ml = reinterpret_cast<const float2*>(p.part_ml);
+    const float2 ml0 = ml[(long)min(lane, ns - 1) * p.num_heads + h];
+    asm volatile("" ::: "memory");  // keeps it ahead of the partials' loads
     float x[kCombineRound];
 #pragma unroll
-    for (int u = 0; u < kCombineRound; ++u) x[u] = u < ns ? src[(long)u * stride] : 0.0f;
+    for (int u = 0; u < kCombineRound; ++u) x[u] = src[(long)min(u, ns - 1) * stride];
     if (threadIdx.x < 64) {
-        const float2* ml = reinterpret_cast<const float2*>(p.part_ml);
-        float mx = -INFINITY;
-        for (int sp = lane; sp < ns; sp += 64) mx = fmaxf(mx, ml[(long)sp * p.num_heads + h].x);
+        float mx = lane < ns ? ml0.x : -INFINITY;
+        for (int sp = lane + 64; sp < ns; sp += 64) mx = fmaxf(mx, ml[(long)sp * p.num_heads + h].x);
         mx = wave_max(mx);
         float ls = 0.0f;
-        for (int sp = lane; sp < ns; sp += 64) {
+        if (lane < ns) {
+            const float w = fast_exp2(ml0.x - mx);
+            s_w[lane] = w;
+            ls += w * ml0.y;
+        }
+        for (int sp = lane + 64; sp < ns; sp += 64) {
             const float2 v = ml[(long)sp * p.num_heads + h];
             const float w = fast_exp2(v.x - mx);
             s_w[sp] = w;
