@@ -140,59 +140,62 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             }
         }
     };
-    // the first tile's loads go out before the q set-up so they overlap it,
-    // and so do the appended row's (the owner would otherwise wait for them
-    // after q is ready).  More than one tile in flight per wave measured
-    // slower at every context length (4096 rows: 12.8 us with four against
-    // 11.7 us with one; 32768 rows: 48.4 us against 43.5 us).
-    if (t0 < t_end) load_tile(t0);
+    // q of the GB heads, rotated at p and pre-scaled, is built once per
+    // workgroup in LDS: one float4 per thread of the first GB*HD/4.  (Loading
+    // each lane's own slice from memory replicated it 64*NW/LPG times per
+    // workgroup, ~80 KB of q and table traffic per CU for the Llama-3-8B
+    // shape.)  Loads complete in issue order, so the set-up's go out first --
+    // q with its table row, then the owner's appended row with its table
+    // entries -- and the first tile right after them: the q rotation waits
+    // for its own loads while the tile is still in flight.  The scheduling
+    // barriers keep that order (left to itself the compiler issued the sin
+    // row after a wait for every earlier load, the tile's included, and
+    // waited again), and the tile is loaded unconditionally (rows past the
+    // end are clamped and never used) so that the waits can count the loads.
+    // More than one tile in flight per wave measured slower at every context
+    // length (4096 rows: 12.8 us with four against 11.7 us with one; 32768
+    // rows: 48.4 us against 43.5 us).
+    const bool rot = p.cos_t != nullptr;  // always set when appending
+    constexpr int NQ4 = GB * HD / 4;
+    static_assert(NQ4 <= 64 * NW, "one q float4 per thread");
+    __shared__ __align__(16) float s_q[GB * HD];
+    const bool qthread = threadIdx.x < NQ4;
+    const int qi = threadIdx.x / (HD / 4);
+    const int qc = threadIdx.x - qi * (HD / 4);
+    float4 xq = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 cq = make_float2(1.0f, 1.0f), sq = make_float2(0.0f, 0.0f);
+    if (qthread) {
+        xq = ld4(p.q + (h0 + qi) * HD + 4 * qc);
+        if (rot) {
+            cq = *reinterpret_cast<const float2*>(p.cos_t + trow + 2 * qc);
+            sq = *reinterpret_cast<const float2*>(p.sin_t + trow + 2 * qc);
+        }
+    }
+    // the owner's lanes rotate the appended k with their dims' table entries
     float4 kn[NV], vn[NV];
+    float2 cr[NV], sr[NV];
     if (append && owner) {
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const int d = 4 * (v * LPG + li);
             kn[v] = ld4(p.k_new + g * HD + d);
             vn[v] = ld4(p.v_new + g * HD + d);
+            const long j = trow + 2 * (v * LPG + li);
+            cr[v] = *reinterpret_cast<const float2*>(p.cos_t + j);
+            sr[v] = *reinterpret_cast<const float2*>(p.sin_t + j);
         }
     }
-
-    // q of the GB heads, rotated at p and pre-scaled, is built once per
-    // workgroup in LDS: one float4 per thread of the first GB*HD/4.  (Loading
-    // each lane's own slice from memory replicated it 64*NW/LPG times per
-    // workgroup, ~80 KB of q and table traffic per CU for the Llama-3-8B
-    // shape, queued behind the first tile's loads: the second half of the
-    // waves got their first tile ~1 us after the first half.)  Every load is
-    // issued before the first use: a load inside the rotate branch would wait
-    // for all earlier loads, the tile's included.
-    const bool rot = p.cos_t != nullptr;  // always set when appending
-    constexpr int NQ4 = GB * HD / 4;
-    static_assert(NQ4 <= 64 * NW, "one q float4 per thread");
-    __shared__ __align__(16) float s_q[GB * HD];
-    if (threadIdx.x < NQ4) {
-        const int i = threadIdx.x / (HD / 4);
-        const int c = threadIdx.x - i * (HD / 4);
-        float4 x = ld4(p.q + (h0 + i) * HD + 4 * c);
-        float2 cq = make_float2(1.0f, 1.0f), sq = make_float2(0.0f, 0.0f);
-        if (rot) {
-            cq = *reinterpret_cast<const float2*>(p.cos_t + trow + 2 * c);
-            sq = *reinterpret_cast<const float2*>(p.sin_t + trow + 2 * c);
-        }
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile(t0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (qthread) {
+        float4 x = xq;
         if (rot) x = rope4_exact(x, cq, sq);
         x.x *= p.scale_log2;
         x.y *= p.scale_log2;
         x.z *= p.scale_log2;
         x.w *= p.scale_log2;
-        *reinterpret_cast<float4*>(&s_q[i * HD + 4 * c]) = x;
-    }
-    // the owner's lanes rotate the appended k with their dims' table entries
-    float2 cr[NV], sr[NV];
-    if (append && owner) {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const long j = trow + 2 * (v * LPG + li);
-            cr[v] = *reinterpret_cast<const float2*>(p.cos_t + j);
-            sr[v] = *reinterpret_cast<const float2*>(p.sin_t + j);
-        }
+        *reinterpret_cast<float4*>(&s_q[qi * HD + 4 * qc]) = x;
     }
     __syncthreads();
     float4 qr[GB][NV];
