@@ -163,7 +163,9 @@ int slm_attn_sync(slm_attn_ctx* ctx);
  * time kernels or would grow a workspace return SLM_ERR_CAPTURE and record
  * nothing (make one uncaptured call first to size workspaces).  Captured
  * launches carry no memset nodes.  Other work on the same stream during the
- * capture (from other libraries) is recorded too. */
+ * capture (from other libraries) is recorded too.  Destroy a graph only after
+ * its replays have finished (slm_attn_sync), and before its context: the
+ * recording holds the context's device buffers. */
 typedef struct slm_attn_graph slm_attn_graph;
 int slm_attn_capture_begin(slm_attn_ctx* ctx);
 int slm_attn_capture_end(slm_attn_ctx* ctx, slm_attn_graph** out);
