@@ -193,3 +193,54 @@ def test_capture_refuses_workspace_growth_then_records_projection():
                 ctx.sync()
                 assert_bitwise(out.cpu().numpy(), eager, f"projection replay {rep}")
                 assert_bitwise(ctx.kv_read(0, 0, 0, 3), eager_k, f"projection replay {rep} K")
+
+
+def test_layer_decode_steps_in_a_graph():
+    """Four one-token steps of the whole transformer block (RMSNorm + Q/K/V,
+    decode attention with split merge, Wo + residual, RMSNorm + gate/up +
+    SwiGLU, down + residual: slm_layer_forward_dev) recorded once and
+    replayed: the residual rows and the appended K/V rows equal the eager
+    steps' bit for bit on every replay."""
+    from test_gpu_layer import Block
+
+    dim, hidden, heads, kvh, msl, pre = 576, 1536, 9, 3, 640, 580
+    kvd = dim // heads * kvh
+    eps = 1e-5
+    steps = 4
+    log(f"layer decode graph: dim {dim} heads {heads}/{kvh} hidden {hidden} after {pre} rows")
+    blk = Block(61, dim, kvd, hidden)
+    try:
+        with P.AttentionContext(dim, heads, kvh, msl, 1, 1e4) as ctx:
+            assert ctx.decode_splits(pre + 1)[0] > 1  # the merge runs in the recording
+            x = torch.from_numpy(gen([62, dim], (msl, dim))).cuda()
+            ctx.layer_forward_dev(0, 0, pre, blk.dev, eps, x[:pre].data_ptr())
+            ctx.sync()
+            x_in = x[pre:pre + steps].clone()
+
+            def run():
+                for st in range(steps):
+                    ctx.layer_forward_dev(0, pre + st, 1, blk.dev, eps, x[pre + st].data_ptr())
+
+            run()
+            ctx.sync()
+            eager = x.cpu().numpy()
+            eager_k = ctx.kv_read(0, 0, pre, steps)
+            eager_v = ctx.kv_read(0, 1, pre, steps)
+            x[pre:pre + steps].copy_(x_in)
+            torch.cuda.synchronize()
+            ctx.capture_begin()
+            run()
+            with ctx.capture_end() as graph:
+                rng = np.random.default_rng(63)
+                for rep in range(3):
+                    x[pre:pre + steps].copy_(x_in)
+                    ctx.kv_write(0, 0, pre, rng.standard_normal((steps, kvd), dtype=np.float32))
+                    ctx.kv_write(0, 1, pre, rng.standard_normal((steps, kvd), dtype=np.float32))
+                    torch.cuda.synchronize()
+                    ctx.graph_launch(graph)
+                    ctx.sync()
+                    assert_bitwise(x.cpu().numpy(), eager, f"layer replay {rep} residual rows")
+                    assert_bitwise(ctx.kv_read(0, 0, pre, steps), eager_k, f"layer replay {rep} K")
+                    assert_bitwise(ctx.kv_read(0, 1, pre, steps), eager_v, f"layer replay {rep} V")
+    finally:
+        blk.close()
