@@ -685,10 +685,13 @@ def bench_workloads(torch, P) -> tuple[list, list]:
         # host call: the dispatch cost without the per-call host round trip
         # (reported as null, with the reason logged, if recording fails)
         graph_ms = None
+        graph = None
         try:
             ctx.capture_begin()
-            run()
-            graph = ctx.capture_end()
+            try:
+                run()
+            finally:  # the stream leaves capture mode whatever happened
+                graph = ctx.capture_end()
             ctx.graph_launch(graph)
             torch.cuda.synchronize()
             e0.record(stream)
@@ -696,9 +699,11 @@ def bench_workloads(torch, P) -> tuple[list, list]:
             e1.record(stream)
             torch.cuda.synchronize()
             graph_ms = e0.elapsed_time(e1)
-            graph.close()
         except P.SlmAttnError as exc:
             log(f"{name}: graph replay not measured: {exc}")
+        finally:
+            if graph is not None:
+                graph.close()
         ctx.profile(True)
         run()
         prof = ctx.profile_read()
