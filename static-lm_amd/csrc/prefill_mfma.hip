@@ -225,19 +225,38 @@ prefill_mfma_kernel(PrefillParams p) {
 
     const float* kg = p.k_cache + g * HD;
     const float* vg = p.v_cache + g * HD;
+    // This thread's NPF float4 of a tile sit at fixed byte offsets from the
+    // tile's first row, so a tile is loaded through a buffer descriptor built
+    // from uniform values (scalar work) plus those offsets: no vector
+    // arithmetic per tile (on this part VALU work of one wave does not overlap
+    // another wave's fp32 MFMAs on the same SIMD, so every VALU instruction in
+    // the loop costs MFMA time).  The descriptor's range ends at row kv_len,
+    // and buffer loads past the range return zeros: the rows past the end
+    // read as zeros without a branch.
+    int t_off[NPF];
+#pragma unroll
+    for (int i = 0; i < NPF; ++i) {
+        const int f = tid + i * NT;
+        t_off[i] = ((f / (HD / 4)) * p.kv_dim + (f % (HD / 4)) * 4) * 4;
+    }
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    auto bload = [](__amdgpu_buffer_rsrc_t r, int off) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        return make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
+                           __uint_as_float(x.w));
+    };
     float4 pk[NPF], pv[NPF];
     auto prefetch = [&](int kb) {
+        const int bytes = (kv_len - kb) * p.kv_dim * 4;  // rows kb..kv_len-1
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(kg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(vg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
 #pragma unroll
         for (int i = 0; i < NPF; ++i) {
-            const int f = tid + i * NT;
-            const int key = kb + f / (HD / 4);
-            const int col = (f % (HD / 4)) * 4;
-            if (f < F4 && key < kv_len) {
-                pk[i] = ld4(kg + (long)key * p.kv_dim + col);
-                pv[i] = ld4(vg + (long)key * p.kv_dim + col);
-            } else {
-                pk[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                pv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (tid + i * NT < F4) {
+                pk[i] = bload(rk, t_off[i]);
+                pv[i] = bload(rv, t_off[i]);
             }
         }
     };
