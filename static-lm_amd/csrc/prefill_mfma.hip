@@ -146,7 +146,10 @@ prefill_mfma_kernel(PrefillParams p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform, and known to be: the per-wave tests below (the causal
+    // mask only on diagonal tiles, rows past the wave's last position) then
+    // compile to branches instead of per-lane selects on every tile
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15;
     const int lg = lane >> 4;
     const int hw = wave % HW;
@@ -314,16 +317,20 @@ prefill_mfma_kernel(PrefillParams p) {
 #pragma unroll
         for (int qt = 0; qt < NQT; ++qt) {
             const int qpos = p.start + q0 + qt * 16 + lr;
+            if (diag) {  // uniform: only tiles that reach past a query of the wave
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (kb + ks * 16 + 4 * lg + r > qpos) s[ks][qt][r] = -INFINITY;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
             float mx = -INFINITY;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float v = s[ks][qt][r];
-                    if (diag && kb + ks * 16 + 4 * lg + r > qpos) v = -INFINITY;
-                    s[ks][qt][r] = v;
-                    mx = fmaxf(mx, v);
-                }
+                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[ks][qt][r]);
             }
             mx = rows_max(mx);
             // the first tile always holds key 0 <= qpos, so m is finite after it
