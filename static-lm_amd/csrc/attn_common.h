@@ -68,13 +68,23 @@ __device__ __forceinline__ float group_sum(float x) {
 // wave) with the VALU lane swaps of gfx950: each swap leaves x[l] and its
 // partner's value in the two outputs, in one order or the other, so the max
 // (sum) of the outputs is the pairwise max (sum).
+// max(a, b) for operands that are not NaN (finite or -inf): one v_max_f32,
+// where fmaxf first canonicalizes operands that come out of a lane swap
+// (two more instructions per call; the compiler folds a median with +inf
+// back into fmaxf)
+__device__ __forceinline__ float max_nonan(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 __device__ __forceinline__ float rows_max(float x) {
     const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                     false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    x = max_nonan(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                     false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return max_nonan(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float rows_sum(float x) {

@@ -342,14 +342,14 @@ prefill_mfma_kernel(PrefillParams p) {
                 for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
                 m[qt] = mn;
             }
-            float ps = 0.0f;
+            float ps = 0.0f;  // starts at the first term (0 + e is e exactly, e >= 0)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float e = __builtin_amdgcn_exp2f(s[ks][qt][r] - m[qt]);
                     s[ks][qt][r] = e;
-                    ps += e;
+                    ps = (ks == 0 && r == 0) ? e : ps + e;
                 }
             }
             l[qt] += ps;
