@@ -5,10 +5,12 @@
 //
 // Tiling.  A workgroup of HW*QS waves owns one query block and HW query heads
 // of one KV head (HW divides kv_mul), so every K/V tile staged in LDS serves
-// HW heads.  Each wave owns 16*NQT query rows of one head.  Keys stream
-// through LDS in tiles of 32 rows (row stride HD+4 floats against bank
-// conflicts); the next tile is prefetched into registers while the current
-// one is in use.
+// HW*QS waves.  Each wave owns 16*NQT query rows of one head.  Keys stream
+// through LDS in tiles of 32 rows.  For hd 128 with four heads per KV head
+// (the Llama-3-8B shape) eight waves share each tile and the tiles go from
+// memory straight into two LDS buffers (buffer loads with the lds bit), with
+// no registers held for the next tile, four waves per SIMD; otherwise the
+// next tile is prefetched into registers while the current one is in use.
 //
 // Transposed products keep softmax state lane-local.  With the 16x16x4 MFMA
 // layout (lane l: A[l%16][l/16], B[l/16][l%16], D[4*(l/16)+r][l%16]):
@@ -26,6 +28,8 @@
 // the running max is reduced across the four lane groups each tile, the
 // running sum stays a per-lane partial until the end.
 #include <math.h>
+
+#include <type_traits>
 
 #include "attn_common.h"
 #include "slm_internal.h"
@@ -98,6 +102,21 @@ struct PrefillLds<256> {
     static __device__ __forceinline__ int k_swz(int) { return 0; }
 };
 
+// Tiles written by buffer->LDS DMA (hd 128): a wave's DMA instruction fills
+// 1 KiB of LDS contiguously, so rows cannot be padded.  Rows are 128 floats;
+// the K chunk index is XORed with k_swz(row) (bits 0-1 and 3 of the row), and
+// lane m reads its two V chunks in the order vrot(m).  Checked conflict-free
+// under the rule above on the CPU, for both readings of the lane grouping.
+template <int HD>
+struct PrefillLdsDma;
+template <>
+struct PrefillLdsDma<128> {
+    static constexpr int LDK = 128;
+    static constexpr int LDV = 128;
+    static __device__ __forceinline__ int k_swz(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
+    static __device__ __forceinline__ int vrot(int m) { return (m >> 3) & 1; }
+};
+
 // First 128-bit chunk lane m reads of its NDT contiguous V dims (NDT a
 // multiple of 4; lane m starts at float m*NDT of its row): with the V row
 // strides above, every cycle's 16 lanes then cover the 64 banks once.
@@ -115,13 +134,17 @@ constexpr int prefill_waves_per_simd() {
     return HD > 128 ? 1 : 2;
 }
 
-template <int HD, int HW, int QS, int NQT, int kKT = 32, int NB = 1, bool PRIO = false>
-__global__ __launch_bounds__(64 * HW * QS, (prefill_waves_per_simd<HD, HW>())) void
+// DMA: K/V tiles go straight from memory to LDS (buffer loads with the lds
+// bit) into two buffers, with no registers held for the next tile; four waves
+// per SIMD.  Otherwise the next tile is prefetched into registers.
+template <int HD, int HW, int QS, int NQT, int kKT = 32, int NB = 1, bool PRIO = false,
+          bool DMA = false>
+__global__ __launch_bounds__(64 * HW * QS, (DMA ? 4 : prefill_waves_per_simd<HD, HW>())) void
 prefill_mfma_kernel(PrefillParams p) {
     constexpr int KS = kKT / 16;  // 16-key sub-tiles per LDS tile
     constexpr int NW = HW * QS;
     constexpr int NT = 64 * NW;
-    using Lds = PrefillLds<HD>;
+    using Lds = std::conditional_t<DMA, PrefillLdsDma<HD>, PrefillLds<HD>>;
     constexpr int LDK = Lds::LDK;
     constexpr int LDV = Lds::LDV;
     constexpr int DPL = HD / 4;   // contiguous head dims per lane group
@@ -141,6 +164,7 @@ prefill_mfma_kernel(PrefillParams p) {
 
     // NB LDS buffers: with two, a tile is stored while the other is read and
     // one barrier per tile suffices
+    static_assert(!DMA || NB == 2, "DMA tiles use two buffers");
     __shared__ __align__(16) float sKb[NB][kKT * LDK];
     __shared__ __align__(16) float sVb[NB][kKT * LDV];
 
@@ -212,19 +236,35 @@ prefill_mfma_kernel(PrefillParams p) {
         }
     }
 
+    // Softmax state per query tile (log2 domain): m, the running max (-inf
+    // before the first key); om, the offset the score accumulators start
+    // from (negm holds -om four times: the QK^T MFMAs then return s - om, and
+    // exp2 takes them without a subtraction); lim, how far a tile's max may
+    // exceed om before the state is rescaled (kLazyRescale once m is set, -inf
+    // before the first tile, which therefore always rescales).
     floatx4 o[NQT][NDT];
-    float m[NQT], l[NQT];
+    float m[NQT], l[NQT], om[NQT], lim[NQT];
+    floatx4 negm[NQT];
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
         m[qt] = -INFINITY;
         l[qt] = 0.0f;
+        om[qt] = 0.0f;
+        lim[qt] = -INFINITY;
+        negm[qt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
 
+    auto vrot_of = [](int m) {
+        if constexpr (DMA)
+            return Lds::vrot(m);
+        else
+            return v_rot<NDT>(m);
+    };
     int v_off[VC];  // this lane's chunk offsets inside its NDT dims
 #pragma unroll
-    for (int c = 0; c < VC; ++c) v_off[c] = 4 * ((c + v_rot<NDT>(lr)) % VC);
+    for (int c = 0; c < VC; ++c) v_off[c] = 4 * ((c + vrot_of(lr)) % VC);
 
     const float* kg = p.k_cache + g * HD;
     const float* vg = p.v_cache + g * HD;
@@ -236,11 +276,26 @@ prefill_mfma_kernel(PrefillParams p) {
     // the loop costs MFMA time).  The descriptor's range ends at row kv_len,
     // and buffer loads past the range return zeros: the rows past the end
     // read as zeros without a branch.
-    int t_off[NPF];
+    constexpr int NI = DMA ? F4 / NT : 1;  // DMA instructions per wave, tile and matrix
+    static_assert(!DMA || F4 % NT == 0, "DMA tiles: whole instructions per wave");
+    int t_off[DMA ? 1 : NPF];
+    int d_off_k[NI], d_off_v[NI];
+    if constexpr (DMA) {
+        // instruction i of this wave fills float4 slots (wave*NI + i)*64 + lane
+        // of a tile; K slot (row r, chunk c) receives chunk c ^ k_swz(r)
 #pragma unroll
-    for (int i = 0; i < NPF; ++i) {
-        const int f = tid + i * NT;
-        t_off[i] = ((f / (HD / 4)) * p.kv_dim + (f % (HD / 4)) * 4) * 4;
+        for (int i = 0; i < NI; ++i) {
+            const int f = (wave * NI + i) * 64 + lane;
+            const int r = f / (HD / 4), c = f % (HD / 4);
+            d_off_k[i] = (r * p.kv_dim + 4 * (c ^ Lds::k_swz(r))) * 4;
+            d_off_v[i] = (r * p.kv_dim + 4 * c) * 4;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NPF; ++i) {
+            const int f = tid + i * NT;
+            t_off[i] = ((f / (HD / 4)) * p.kv_dim + (f % (HD / 4)) * 4) * 4;
+        }
     }
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     auto bload = [](__amdgpu_buffer_rsrc_t r, int off) {
@@ -248,41 +303,45 @@ prefill_mfma_kernel(PrefillParams p) {
         return make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
                            __uint_as_float(x.w));
     };
-    float4 pk[NPF], pv[NPF];
-    auto prefetch = [&](int kb) {
+    float4 pk[DMA ? 1 : NPF], pv[DMA ? 1 : NPF];
+    auto prefetch = [&](int kb, int buf) __attribute__((always_inline)) {
         const int bytes = (kv_len - kb) * p.kv_dim * 4;  // rows kb..kv_len-1
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(kg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(vg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
+        if constexpr (DMA) {
+            // Issued as inline assembly: the compiler then sees no LDS store
+            // here, so it does not make the current tile's LDS reads wait for
+            // this DMA (it cannot tell the two buffers apart); the vmcnt(0)
+            // wait and the barrier ahead of the next tile order them instead.
+            // M0 holds the wave's LDS destination; lane l's 16 bytes land at
+            // M0 + 16*l.
 #pragma unroll
-        for (int i = 0; i < NPF; ++i) {
-            if (tid + i * NT < F4) {
-                pk[i] = bload(rk, t_off[i]);
-                pv[i] = bload(rv, t_off[i]);
+            for (int i = 0; i < NI; ++i) {
+                const unsigned lk = (unsigned)(unsigned long)(
+                    __attribute__((address_space(3))) float*)&sKb[buf][(wave * NI + i) * 256];
+                const unsigned lv = (unsigned)(unsigned long)(
+                    __attribute__((address_space(3))) float*)&sVb[buf][(wave * NI + i) * 256];
+                asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(d_off_k[i]),
+                             "s"(rk), "{m0}"(lk) : "memory");
+                asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(d_off_v[i]),
+                             "s"(rv), "{m0}"(lv) : "memory");
+            }
+        } else {
+            (void)buf;
+#pragma unroll
+            for (int i = 0; i < NPF; ++i) {
+                if (tid + i * NT < F4) {
+                    pk[i] = bload(rk, t_off[i]);
+                    pv[i] = bload(rv, t_off[i]);
+                }
             }
         }
     };
-    prefetch(0);
 
-    for (int it = 0; it < n_tiles; ++it) {
-        const int kb = it * kKT;
-        float* sK = sKb[it % NB];
-        float* sV = sVb[it % NB];
-        if (NB == 1) __syncthreads();  // every wave is done with the previous tile
-#pragma unroll
-        for (int i = 0; i < NPF; ++i) {
-            const int f = tid + i * NT;
-            if (f < F4) {
-                const int r = f / (HD / 4), ch = f % (HD / 4);
-                *reinterpret_cast<float4*>(&sK[r * LDK + 4 * (ch ^ Lds::k_swz(r))]) = pk[i];
-                *reinterpret_cast<float4*>(&sV[r * LDV + 4 * ch]) = pv[i];
-            }
-        }
-        __syncthreads();
-        if (it + 1 < n_tiles) prefetch(kb + kKT);
-        if (wave_rows == 0 || kb > wave_last_pos) continue;  // wave-uniform
-
+    // One key tile: S^T = K.Q^T, causal mask, online softmax, O^T += V^T.P^T.
+    auto attend = [&](int kb, const float* sK, const float* sV) __attribute__((always_inline)) {
         // S^T tiles [key sub-tile][query tile]; the KS*NQT accumulators are
         // updated round-robin so consecutive MFMAs never depend on each other
         if (PRIO) __builtin_amdgcn_s_setprio(1);
@@ -290,7 +349,7 @@ prefill_mfma_kernel(PrefillParams p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int qt = 0; qt < NQT; ++qt) s[ks][qt] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int qt = 0; qt < NQT; ++qt) s[ks][qt] = negm[qt];
 #pragma unroll
         for (int c = 0; c < DPL / 4; ++c) {
             float4 kf[KS];
@@ -332,22 +391,31 @@ prefill_mfma_kernel(PrefillParams p) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[ks][qt][r]);
             }
-            mx = rows_max(mx);
-            // the first tile always holds key 0 <= qpos, so m is finite after it
-            if (__any(mx > m[qt] + kLazyRescale)) {  // wave-uniform
-                const float mn = fmaxf(m[qt], mx);
+            mx = rows_max(mx);  // of s - om
+            // the first tile always holds key 0 <= qpos, so mx is finite there
+            if (__any(mx > lim[qt])) {  // wave-uniform
+                const float mn = fmaxf(m[qt], mx + om[qt]);
                 const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
                 l[qt] *= alpha;
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+                const float d = mn - om[qt];  // this tile's scores move to the new offset
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[ks][qt][r] -= d;
+                }
                 m[qt] = mn;
+                om[qt] = mn;
+                lim[qt] = kLazyRescale;
+                negm[qt] = floatx4{-mn, -mn, -mn, -mn};
             }
             float ps = 0.0f;  // starts at the first term (0 + e is e exactly, e >= 0)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float e = __builtin_amdgcn_exp2f(s[ks][qt][r] - m[qt]);
+                    const float e = __builtin_amdgcn_exp2f(s[ks][qt][r]);
                     s[ks][qt][r] = e;
                     ps = (ks == 0 && r == 0) ? e : ps + e;
                 }
@@ -397,6 +465,48 @@ prefill_mfma_kernel(PrefillParams p) {
             }
         }
         if (PRIO) __builtin_amdgcn_s_setprio(0);
+    };
+
+    prefetch(0, 0);
+    if constexpr (DMA) {
+        // Two tiles per trip, so each tile's buffer is a compile-time constant:
+        // the LDS read addresses are then loop-invariant registers plus
+        // immediate offsets instead of being recomputed per tile.
+        auto step = [&](int it, auto buf_c) __attribute__((always_inline)) {
+            constexpr int buf = decltype(buf_c)::value;
+            // this wave's DMA of tile it has landed; after the barrier every
+            // wave's has, and every wave is done with the other buffer
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (it + 1 < n_tiles) prefetch((it + 1) * kKT, buf ^ 1);
+            const int kb = it * kKT;
+            if (wave_rows == 0 || kb > wave_last_pos) return;  // wave-uniform
+            attend(kb, sKb[buf], sVb[buf]);
+        };
+        for (int it = 0; it < n_tiles; it += 2) {
+            step(it, std::integral_constant<int, 0>());
+            if (it + 1 < n_tiles) step(it + 1, std::integral_constant<int, 1>());
+        }
+    } else {
+        for (int it = 0; it < n_tiles; ++it) {
+            const int kb = it * kKT;
+            float* sK = sKb[it % NB];
+            float* sV = sVb[it % NB];
+            if (NB == 1) __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+            for (int i = 0; i < NPF; ++i) {
+                const int f = tid + i * NT;
+                if (f < F4) {
+                    const int r = f / (HD / 4), ch = f % (HD / 4);
+                    *reinterpret_cast<float4*>(&sK[r * LDK + 4 * (ch ^ Lds::k_swz(r))]) = pk[i];
+                    *reinterpret_cast<float4*>(&sV[r * LDV + 4 * ch]) = pv[i];
+                }
+            }
+            __syncthreads();
+            if (it + 1 < n_tiles) prefetch(kb + kKT, 0);
+            if (wave_rows == 0 || kb > wave_last_pos) continue;  // wave-uniform
+            attend(kb, sK, sV);
+        }
     }
 
     // normalise and store
@@ -413,7 +523,7 @@ prefill_mfma_kernel(PrefillParams p) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int m = 4 * lg + r;
-                    const int rot = v_rot<NDT>(m);
+                    const int rot = vrot_of(m);
 #pragma unroll
                     for (int c = 0; c < VC; ++c) {
                         float4 x;
@@ -469,6 +579,18 @@ hipError_t launch_t(const Shape& s, const PrefillParams& pp, hipStream_t st) {
 template <int HD>
 hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
     const Tiling t = pick_tiling(s.kv_mul);
+    if constexpr (HD == 128) {
+        if (t.hw == 4) {
+            // four heads of one KV head and two 16-row query blocks per
+            // workgroup (8 waves), DMA-fed LDS tiles: the same K/V tile serves
+            // eight waves, and two 64 KiB workgroups fit a CU's LDS
+            constexpr int QB = 32;
+            const int n_qb = (pp.n + QB - 1) / QB;
+            hipLaunchKernelGGL((prefill_mfma_kernel<128, 4, 2, 1, 32, 2, false, true>),
+                               dim3(n_qb * (s.num_heads / 4)), dim3(512), 0, st, pp);
+            return hipGetLastError();
+        }
+    }
     if (t.hw == 4) return launch_t<HD, 4, 1>(s, pp, st);
     if (t.hw == 3) return launch_t<HD, 3, 1>(s, pp, st);
     if (t.hw == 2) return launch_t<HD, 2, 2>(s, pp, st);
