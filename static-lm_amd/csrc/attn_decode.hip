@@ -27,10 +27,11 @@
 // fences, which on this part write back and invalidate the whole L2: a
 // second small kernel is cheaper.)
 //
-// The workgroup owning position p does not read row p back: it rotates k in
-// registers with the reference's f32 arithmetic (no FMA contraction), stores
-// K[p] and V[p] (bit-exact with the reference), and seeds its state with
-// them.  No other workgroup reads row p.
+// The workgroup owning position p does not read row p back: after its loop,
+// its wave 0 rotates k in registers with the reference's f32 arithmetic (no
+// FMA contraction), stores K[p] and V[p] (bit-exact with the reference), and
+// adds row p to its first lane group's state as one more position.  No other
+// workgroup reads row p.
 #include <hip/hip_ext.h>
 #include <math.h>
 
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     const int t_end = append ? p.pos : seq_len;  // rows read from the cache
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform, and known to be
     const int li = lane % LPG;
     const int lg = lane / LPG;
     const long trow = (long)p.pos * p.half;
@@ -145,9 +146,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // each lane's own slice from memory replicated it 64*NW/LPG times per
     // workgroup, ~80 KB of q and table traffic per CU for the Llama-3-8B
     // shape.)  Loads complete in issue order, so the set-up's go out first --
-    // q with its table row, then the owner's appended row with its table
-    // entries -- and the first tile right after them: the q rotation waits
-    // for its own loads while the tile is still in flight.  The scheduling
+    // q with its table row -- and the first tile right after them: the q
+    // rotation waits for its own loads while the tile is still in flight.
+    // The scheduling
     // barriers keep that order (left to itself the compiler issued the sin
     // row after a wait for every earlier load, the tile's included, and
     // waited again), and the tile is loaded unconditionally (rows past the
@@ -171,22 +172,45 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             sq = *reinterpret_cast<const float2*>(p.sin_t + trow + 2 * qc);
         }
     }
-    // the owner's lanes rotate the appended k with their dims' table entries
-    float4 kn[NV], vn[NV];
-    float2 cr[NV], sr[NV];
-    if (append && owner) {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const int d = 4 * (v * LPG + li);
-            kn[v] = ld4(p.k_new + g * HD + d);
-            vn[v] = ld4(p.v_new + g * HD + d);
-            const long j = trow + 2 * (v * LPG + li);
-            cr[v] = *reinterpret_cast<const float2*>(p.cos_t + j);
-            sr[v] = *reinterpret_cast<const float2*>(p.sin_t + j);
-        }
-    }
     __builtin_amdgcn_sched_barrier(0);
     load_tile(t0);
+    // The appended row (k, v and the table entries of its dims) is used only
+    // by wave 0 of the owner, after the loop.  Its loads go out behind the
+    // first tile, from every wave, through buffer descriptors whose range is
+    // empty except in that wave (out-of-range loads return zeros and touch no
+    // memory): with the same loads on every path the compiler waits for q
+    // and the first tile alone.  (Issued ahead of the tile by the owner only,
+    // they were waited for at the set-up barrier -- loads complete in issue
+    // order -- and the owner's workgroups passed it 1.4 us after the others.)
+    const bool app_wave = append && owner && wave == 0;  // wave-uniform
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const int row_bytes = app_wave ? HD * 4 : 0;
+    const int tab_bytes = app_wave ? HD * 2 : 0;  // half a table row: HD/2 floats
+    const __amdgpu_buffer_rsrc_t rkn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.k_new + g * HD), 0, row_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rvn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.v_new + g * HD), 0, row_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rcos = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.cos_t + trow), 0, tab_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsin = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.sin_t + trow), 0, tab_bytes, 0x00020000);
+    float4 kn[NV], vn[NV];
+    float2 cr[NV], sr[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const int d = 4 * (v * LPG + li);  // this lane's dims of the row
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rkn, 4 * d, 0, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rvn, 4 * d, 0, 0);
+        const u32x2 c = __builtin_amdgcn_raw_buffer_load_b64(rcos, 2 * d, 0, 0);
+        const u32x2 e = __builtin_amdgcn_raw_buffer_load_b64(rsin, 2 * d, 0, 0);
+        kn[v] = make_float4(__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z),
+                            __uint_as_float(a.w));
+        vn[v] = make_float4(__uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z),
+                            __uint_as_float(b.w));
+        cr[v] = make_float2(__uint_as_float(c.x), __uint_as_float(c.y));
+        sr[v] = make_float2(__uint_as_float(e.x), __uint_as_float(e.y));
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (qthread) {
         float4 x = xq;
@@ -216,42 +240,37 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int v = 0; v < NV; ++v) o[i][v] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
-    if (append && owner) {
-        // the appended row, from registers
-        const bool writer = (gy % nhb) == 0 && wave == 0 && lg == 0;
+    // The first tile, loaded with the set-up, is attended outside the loop:
+    // there the compiler knows the appended row's loads are younger and waits
+    // for the tile alone (merged with the loop's own wait, it waited for
+    // most of them too).
+    if (t0 < t_end) attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
+    for (int tb = t0 + t_step; tb < t_end; tb += t_step) {
+        load_tile(tb);
+        attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
+    }
+    if (app_wave) {
+        // Row p: k rotated at p with the reference's f32 arithmetic (no FMA
+        // contraction), K[p] and V[p] stored bit-exact, then one more
+        // position of lane group 0's state.
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const int d = 4 * (v * LPG + li);
-            kn[v] = rope4_exact(kn[v], cr[v], sr[v]);
-            if (writer) {
+        for (int v = 0; v < NV; ++v) kn[v] = rope4_exact(kn[v], cr[v], sr[v]);
+        if (lg == 0 && (gy % nhb) == 0) {
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const int d = 4 * (v * LPG + li);
                 *reinterpret_cast<float4*>(p.k_cache + (long)p.pos * p.kv_dim + g * HD + d) = kn[v];
                 *reinterpret_cast<float4*>(p.v_cache + (long)p.pos * p.kv_dim + g * HD + d) = vn[v];
             }
         }
-        const bool seed = wave == 0 && lg == 0;
+        float4 kt[1][NV], vt[1][NV];
 #pragma unroll
-        for (int i = 0; i < GB; ++i) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int v = 0; v < NV; ++v) {
-                acc = fmaf(qr[i][v].x, kn[v].x, acc);
-                acc = fmaf(qr[i][v].y, kn[v].y, acc);
-                acc = fmaf(qr[i][v].z, kn[v].z, acc);
-                acc = fmaf(qr[i][v].w, kn[v].w, acc);
-            }
-            acc = group_sum<LPG>(acc);
-            if (seed) {
-                m[i] = acc;
-                l[i] = 1.0f;
-#pragma unroll
-                for (int v = 0; v < NV; ++v) o[i][v] = vn[v];
-            }
+        for (int v = 0; v < NV; ++v) {
+            kt[0][v] = kn[v];
+            vt[0][v] = vn[v];
         }
-    }
-
-    for (int tb = t0; tb < t_end; tb += t_step) {
-        if (tb != t0) load_tile(tb);
-        attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
+        const bool mine[1] = {lg == 0};
+        attend_tile<LPG, NV, GB, 1>(qr, kt, vt, mine, m, l, o);
     }
     // Merge of the workgroup's NS lane-group states per head: the workgroup
     // max M over the lane groups' maxima (max over the wave's lane groups by
