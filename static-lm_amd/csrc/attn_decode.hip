@@ -272,73 +272,162 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         const bool mine[1] = {lg == 0};
         attend_tile<LPG, NV, GB, 1>(qr, kt, vt, mine, m, l, o);
     }
-    // Merge of the workgroup's NS lane-group states per head: the workgroup
-    // max M over the lane groups' maxima (max over the wave's lane groups by
-    // lane swaps, then over the waves through LDS), every lane group scales
-    // its (l, o) once by 2^(m - M) into its own LDS slot, and each thread sums
-    // the slots of one (head, dim) in slot order.  (Merging pairs of lane
-    // groups in registers first, with a scale per pair and round, cost ~360
-    // VALU ops per wave: ~1.5 us between a workgroup's last wave leaving the
-    // loop and the barrier, at two waves per SIMD.)
-    constexpr int NS = NW * GPW;  // lane-group states per workgroup
-    __shared__ float s_mw[NW][GB];
-    __shared__ __align__(16) float s_o[NS][GB][HD];
-    __shared__ float s_l[GB][NS];
-    float mg[GB];
+    if constexpr (GPW == 4) {
+        // Merge in two levels.  In the wave: each lane group scales its (l, o)
+        // by 2^(m - Mw), Mw the wave's max per head (lane swaps), and two
+        // rounds of lane swaps sum the four lane groups -- register pairs (f,
+        // f+F/2) across the wave's halves, then (f, f+F/4) across rows -- so
+        // that row r of register f ends holding flat element r*F/4 + f of o
+        // summed over the rows (for four heads: head r, this lane's dims).
+        // 24 swaps and 24 adds for the Llama-3-8B shape, done by each wave as
+        // soon as its loop ends.  In the workgroup: one barrier, then each
+        // thread combines one (head, dim) over the waves in wave order.  (All
+        // 32 lane-group states through LDS with two barriers took ~1.5 us
+        // after the last wave's loop at every context length.)
+        constexpr int F = GB * NV * 4;  // floats of o per lane
+        static_assert(F % 4 == 0, "two swap rounds need F a multiple of 4");
+        float mw[GB], lw[GB], of[F];
 #pragma unroll
-    for (int i = 0; i < GB; ++i) mg[i] = groups_max<LPG>(m[i]);
-    if (lane == 0) {
+        for (int i = 0; i < GB; ++i) {
+            mw[i] = rows_max(m[i]);  // -inf when the wave saw no position
+            const float mu = (mw[i] == -INFINITY) ? 0.0f : mw[i];
+            const float sc = fast_exp2(m[i] - mu);  // 0 for a lane group that saw nothing
+            lw[i] = rows_sum(l[i] * sc);
 #pragma unroll
-        for (int i = 0; i < GB; ++i) s_mw[wave][i] = mg[i];
-    }
-    __syncthreads();
-    float mwg[GB];  // the workgroup max per head, 0 when no position was seen
-#pragma unroll
-    for (int i = 0; i < GB; ++i) {
-        float mx = s_mw[0][i];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_mw[w][i]);
-        mwg[i] = mx;
-    }
-    const int slot = wave * GPW + lg;
-#pragma unroll
-    for (int i = 0; i < GB; ++i) {
-        const float mu = (mwg[i] == -INFINITY) ? 0.0f : mwg[i];
-        const float w = fast_exp2(m[i] - mu);  // 0 for a lane group that saw nothing
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            float4 x = o[i][v];
-            x.x *= w;
-            x.y *= w;
-            x.z *= w;
-            x.w *= w;
-            *reinterpret_cast<float4*>(&s_o[slot][i][4 * (v * LPG + li)]) = x;
+            for (int v = 0; v < NV; ++v) {
+                of[(i * NV + v) * 4 + 0] = o[i][v].x * sc;
+                of[(i * NV + v) * 4 + 1] = o[i][v].y * sc;
+                of[(i * NV + v) * 4 + 2] = o[i][v].z * sc;
+                of[(i * NV + v) * 4 + 3] = o[i][v].w * sc;
+            }
         }
-        if (li == 0) s_l[i][slot] = l[i] * w;
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < GB * HD; idx += 64 * NW) {
-        const int i = idx / HD;
-        const int d = idx - i * HD;
-        float mx = mwg[0];
+        float z[F / 2], wv[F / 4];
 #pragma unroll
-        for (int j = 1; j < GB; ++j)
-            if (i == j) mx = mwg[j];
-        float acc_o = 0.0f, acc_l = 0.0f;
-#pragma unroll
-        for (int sl = 0; sl < NS; ++sl) {
-            acc_o += s_o[sl][i][d];
-            acc_l += s_l[i][sl];
+        for (int f = 0; f < F / 2; ++f) {
+            const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(of[f]),
+                                                            __float_as_uint(of[f + F / 2]), false,
+                                                            false);
+            z[f] = __uint_as_float(a[0]) + __uint_as_float(a[1]);
         }
-        const int h = h0 + i;
-        if (p.n_splits == 1) {
-            p.out[h * HD + d] = acc_o / acc_l;
-        } else {
-            const long pi = (long)split * p.num_heads + h;
-            p.part_o[pi * HD + d] = acc_o;
-            if (d == 0) {
-                p.part_ml[pi * 2] = mx;
-                p.part_ml[pi * 2 + 1] = acc_l;
+#pragma unroll
+        for (int f = 0; f < F / 4; ++f) {
+            const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(z[f]),
+                                                            __float_as_uint(z[f + F / 4]), false,
+                                                            false);
+            wv[f] = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+        }
+        __shared__ __align__(16) float s_ow[NW][GB * HD];
+        __shared__ float s_mx[NW][GB];
+        __shared__ float s_lw[NW][GB];
+#pragma unroll
+        for (int f = 0; f < F / 4; ++f) {
+            const int e = lg * (F / 4) + f;  // flat element of o held by this row
+            const int i = e / (NV * 4), v = (e / 4) % NV, c = e % 4;
+            s_ow[wave][i * HD + 4 * (v * LPG + li) + c] = wv[f];
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < GB; ++i) {
+                s_mx[wave][i] = mw[i];
+                s_lw[wave][i] = lw[i];
+            }
+        }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < GB * HD; idx += 64 * NW) {
+            const int i = idx / HD;
+            const int d = idx - i * HD;
+            float mx = s_mx[0][i];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_mx[w][i]);
+            const float mu = (mx == -INFINITY) ? 0.0f : mx;
+            float acc_o = 0.0f, acc_l = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const float e = fast_exp2(s_mx[w][i] - mu);  // 0 for a wave that saw nothing
+                acc_o += e * s_ow[w][idx];
+                acc_l += e * s_lw[w][i];
+            }
+            const int h = h0 + i;
+            if (p.n_splits == 1) {
+                p.out[h * HD + d] = acc_o / acc_l;
+            } else {
+                const long pi = (long)split * p.num_heads + h;
+                p.part_o[pi * HD + d] = acc_o;
+                if (d == 0) {
+                    p.part_ml[pi * 2] = mx;
+                    p.part_ml[pi * 2 + 1] = acc_l;
+                }
+            }
+        }
+    } else {
+        // Merge of the workgroup's NS lane-group states per head: the workgroup
+        // max M over the lane groups' maxima (max over the wave's lane groups by
+        // lane swaps, then over the waves through LDS), every lane group scales
+        // its (l, o) once by 2^(m - M) into its own LDS slot, and each thread sums
+        // the slots of one (head, dim) in slot order.  (Merging pairs of lane
+        // groups in registers first, with a scale per pair and round, cost ~360
+        // VALU ops per wave: ~1.5 us between a workgroup's last wave leaving the
+        // loop and the barrier, at two waves per SIMD.)
+        constexpr int NS = NW * GPW;  // lane-group states per workgroup
+        __shared__ float s_mw[NW][GB];
+        __shared__ __align__(16) float s_o[NS][GB][HD];
+        __shared__ float s_l[GB][NS];
+        float mg[GB];
+#pragma unroll
+        for (int i = 0; i < GB; ++i) mg[i] = groups_max<LPG>(m[i]);
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < GB; ++i) s_mw[wave][i] = mg[i];
+        }
+        __syncthreads();
+        float mwg[GB];  // the workgroup max per head, 0 when no position was seen
+#pragma unroll
+        for (int i = 0; i < GB; ++i) {
+            float mx = s_mw[0][i];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_mw[w][i]);
+            mwg[i] = mx;
+        }
+        const int slot = wave * GPW + lg;
+#pragma unroll
+        for (int i = 0; i < GB; ++i) {
+            const float mu = (mwg[i] == -INFINITY) ? 0.0f : mwg[i];
+            const float w = fast_exp2(m[i] - mu);  // 0 for a lane group that saw nothing
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float4 x = o[i][v];
+                x.x *= w;
+                x.y *= w;
+                x.z *= w;
+                x.w *= w;
+                *reinterpret_cast<float4*>(&s_o[slot][i][4 * (v * LPG + li)]) = x;
+            }
+            if (li == 0) s_l[i][slot] = l[i] * w;
+        }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < GB * HD; idx += 64 * NW) {
+            const int i = idx / HD;
+            const int d = idx - i * HD;
+            float mx = mwg[0];
+#pragma unroll
+            for (int j = 1; j < GB; ++j)
+                if (i == j) mx = mwg[j];
+            float acc_o = 0.0f, acc_l = 0.0f;
+#pragma unroll
+            for (int sl = 0; sl < NS; ++sl) {
+                acc_o += s_o[sl][i][d];
+                acc_l += s_l[i][sl];
+            }
+            const int h = h0 + i;
+            if (p.n_splits == 1) {
+                p.out[h * HD + d] = acc_o / acc_l;
+            } else {
+                const long pi = (long)split * p.num_heads + h;
+                p.part_o[pi * HD + d] = acc_o;
+                if (d == 0) {
+                    p.part_ml[pi * 2] = mx;
+                    p.part_ml[pi * 2 + 1] = acc_l;
+                }
             }
         }
     }
