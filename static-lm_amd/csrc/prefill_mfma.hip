@@ -580,12 +580,17 @@ template <int HD>
 hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
     const Tiling t = pick_tiling(s.kv_mul);
     if constexpr (HD == 128) {
-        if (t.hw == 4) {
-            // four heads of one KV head and two 16-row query blocks per
-            // workgroup (8 waves), DMA-fed LDS tiles: the same K/V tile serves
-            // eight waves, and two 64 KiB workgroups fit a CU's LDS
-            constexpr int QB = 32;
-            const int n_qb = (pp.n + QB - 1) / QB;
+        // Four heads of one KV head and two 16-row query blocks per workgroup
+        // (8 waves), DMA-fed LDS tiles: the same K/V tile serves eight waves,
+        // and two 64 KiB workgroups fit a CU's LDS.  Its grid is half the
+        // other kernel's, so it runs only when that still gives four
+        // workgroups per CU: measured for the Llama-3-8B shape, the DMA kernel
+        // against the register-prefetch one took 73.5 / 48.8 us at 512 rows,
+        // 141 / 114 at 1024, 388 / 324 at 2048, 625 / 619-637 at 3072 and
+        // 985-991 / 1025 at 4096.
+        constexpr int QB = 32;
+        const int n_qb = (pp.n + QB - 1) / QB;
+        if (t.hw == 4 && (long)n_qb * (s.num_heads / 4) >= 4L * s.cus) {
             hipLaunchKernelGGL((prefill_mfma_kernel<128, 4, 2, 1, 32, 2, false, true>),
                                dim3(n_qb * (s.num_heads / 4)), dim3(512), 0, st, pp);
             return hipGetLastError();
