@@ -148,11 +148,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // shape.)  Loads complete in issue order, so the set-up's go out first --
     // q with its table row -- and the first tile right after them: the q
     // rotation waits for its own loads while the tile is still in flight.
-    // The scheduling
-    // barriers keep that order (left to itself the compiler issued the sin
-    // row after a wait for every earlier load, the tile's included, and
-    // waited again), and the tile is loaded unconditionally (rows past the
-    // end are clamped and never used) so that the waits can count the loads.
+    // The scheduling barriers keep that order (left to itself the compiler
+    // issued the sin row after a wait for every earlier load, the tile's
+    // included, and waited again), and the tile is loaded unconditionally
+    // (rows past the end are clamped and never used) so that the waits can
+    // count the loads.
     // More than one tile in flight per wave measured slower at every context
     // length (4096 rows: 12.8 us with four against 11.7 us with one; 32768
     // rows: 48.4 us against 43.5 us).
