@@ -245,6 +245,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // for the tile alone (merged with the loop's own wait, it waited for
     // most of them too).
     if (t0 < t_end) attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
+    // The second half of the waves issues its first loads after the first
+    // half's and falls further behind over the loop (each shares a SIMD with
+    // an older wave of the first half): at 32k rows its loops ended 1.1-1.4 us
+    // later.  Raising its issue priority for the loop took 0.3 us off a 32k
+    // layer-step and 0.14 us off a 4096-row one (means of five interleaved
+    // runs); from the kernel's start, or alternating per tile, it did not.
+    if (wave >= NW / 2) __builtin_amdgcn_s_setprio(1);
     for (int tb = t0 + t_step; tb < t_end; tb += t_step) {
         load_tile(tb);
         attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
