@@ -413,6 +413,9 @@ DECODE_SHAPES = [
     (768, 8, 8),     # hd 96
     (4096, 32, 8),   # hd 128, kv_mul 4 (Llama-3-8B)
     (2048, 16, 2),   # hd 128, kv_mul 8
+    (1536, 12, 4),   # hd 128, kv_mul 3: three heads per workgroup
+    (1024, 8, 4),    # hd 128, kv_mul 2: two heads per workgroup
+    (768, 6, 6),     # hd 128, MHA: one head per workgroup
     (1024, 4, 4),    # hd 256
 ]
 
@@ -422,7 +425,8 @@ def test_decode_split_tiles_across_shapes(dim, heads, kv_heads):
     """Decode with append at positions where split ownership changes.
 
     Split s of n reads tiles s, s+n, ... of the cache; the split holding row p's
-    tile writes row p and seeds its state with it.  While the split count is
+    tile writes row p and adds it to its state after its loop (with no cache
+    tile at all when row p starts the split's only tile).  While the split count is
     below its cap there is one tile per split and the last split owns row p;
     beyond it ownership rotates.  Positions: the shortest sequence that splits,
     and, past the cap, the first row of a tile held by split 0 and by split 1,
