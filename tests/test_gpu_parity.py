@@ -111,6 +111,31 @@ def test_llama3_shape_prefill4096_then_decode():
         assert_bitwise(ctx.kv_read(0, 0, n, w.decode), om.k_cache(0)[n:rows], "K rows")
 
 
+def test_llama3_shape_prefill4096_continued_at_300():
+    # A 4096-row prefill continued at start 300: on 256 CUs this size and
+    # shape take the prefill kernel that stages K/V tiles by DMA, whose key
+    # range then starts past the first tile boundary.  K/V rows bit for bit,
+    # sampled rows against the oracle over the same cache.
+    w = WORKLOADS["c4"]
+    cfg = w.cfg()
+    s0, n = 300, 4096
+    rows = s0 + n
+    q = gen([91, w.dim], (rows, w.dim))
+    k = gen([92, w.dim], (rows, w.kv_dim))
+    v = gen([93, w.dim], (rows, w.kv_dim))
+    with make_ctx(w) as ctx:
+        log(f"c4 shape: prefill {s0} rows, then {n} more at start {s0}")
+        ctx.prefill(0, 0, q[:s0], k[:s0], v[:s0])
+        g = ctx.prefill(0, s0, q[s0:], k[s0:], v[s0:])
+        om = orc.OracleModel(cfg)
+        om.append(0, 0, k, v)
+        assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
+        for b in (0, 1, 15, 16, 19, 20, 31, 32, 1000, 2047, 4095):
+            p = s0 + b
+            assert_close(g[b], om.attend(0, q[p], p), what=f"continued prefill row {p}")
+
+
 def test_long_context_decode_131072():
     w = WORKLOADS["c5"]
     cfg = w.cfg()
