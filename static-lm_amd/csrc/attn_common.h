@@ -250,6 +250,20 @@ __device__ __forceinline__ float groups_max(float x) {
     }
 }
 
+// Sum over the lane groups of a wave (lanes with equal index inside their
+// LPG-lane group), pairs of groups LPG apart first; every lane gets the
+// result (the two lanes of a pair add the same two values).
+template <int LPG>
+__device__ __forceinline__ float groups_sum(float x) {
+    if constexpr (LPG < 64) {
+        float a, b;
+        lane_pair<LPG>(x, a, b);
+        return groups_sum<2 * LPG>(a + b);
+    } else {
+        return x;
+    }
+}
+
 // Merges the online-softmax states of lane groups OFF apart, then the next
 // level up to the whole wave.
 template <int OFF, int NV, int GB>

@@ -279,27 +279,35 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         const bool mine[1] = {lg == 0};
         attend_tile<LPG, NV, GB, 1>(qr, kt, vt, mine, m, l, o);
     }
-    if constexpr (GPW == 4) {
+    constexpr int F = GB * NV * 4;  // floats of o per lane
+    if constexpr ((GPW == 4 || GPW == 8) && F % GPW == 0) {
         // Merge in two levels.  In the wave: each lane group scales its (l, o)
-        // by 2^(m - Mw), Mw the wave's max per head (lane swaps), and two
-        // rounds of lane swaps sum the four lane groups -- register pairs (f,
-        // f+F/2) across the wave's halves, then (f, f+F/4) across rows -- so
-        // that row r of register f ends holding flat element r*F/4 + f of o
-        // summed over the rows (for four heads: head r, this lane's dims).
-        // 24 swaps and 24 adds for the Llama-3-8B shape, done by each wave as
-        // soon as its loop ends.  In the workgroup: one barrier, then each
-        // thread combines one (head, dim) over the waves in wave order.  (All
-        // 32 lane-group states through LDS with two barriers took ~1.5 us
-        // after the last wave's loop at every context length.)
-        constexpr int F = GB * NV * 4;  // floats of o per lane
-        static_assert(F % 4 == 0, "two swap rounds need F a multiple of 4");
+        // by 2^(m - Mw), Mw the wave's max per head, and rounds of lane
+        // exchanges sum the lane groups -- register pairs (f, f+F/2) across
+        // the wave's halves (v_permlane32_swap), (f, f+F/4) across 16-lane
+        // rows (v_permlane16_swap) and, with 8 lanes per position, (f, f+F/8)
+        // across the two halves of a row (DPP row_ror:8) -- so that lane group
+        // g of register f ends holding flat element g*F/GPW + f of o summed
+        // over the groups (for the Llama-3-8B shape: head g, the lane's dims).
+        // 24 swaps and 24 adds there, done by each wave as soon as its loop
+        // ends.  In the workgroup: one barrier, then each thread combines one
+        // (head, dim) over the waves in wave order.  (All lane-group states
+        // through LDS with two barriers took ~1.5 us after the last wave's
+        // loop at every context length.)
         float mw[GB], lw[GB], of[F];
 #pragma unroll
         for (int i = 0; i < GB; ++i) {
-            mw[i] = rows_max(m[i]);  // -inf when the wave saw no position
+            // -inf when the wave saw no position
+            if constexpr (GPW == 4)
+                mw[i] = rows_max(m[i]);
+            else
+                mw[i] = groups_max<LPG>(m[i]);
             const float mu = (mw[i] == -INFINITY) ? 0.0f : mw[i];
             const float sc = fast_exp2(m[i] - mu);  // 0 for a lane group that saw nothing
-            lw[i] = rows_sum(l[i] * sc);
+            if constexpr (GPW == 4)
+                lw[i] = rows_sum(l[i] * sc);
+            else
+                lw[i] = groups_sum<LPG>(l[i] * sc);
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
                 of[(i * NV + v) * 4 + 0] = o[i][v].x * sc;
@@ -308,7 +316,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
                 of[(i * NV + v) * 4 + 3] = o[i][v].w * sc;
             }
         }
-        float z[F / 2], wv[F / 4];
+        float z[F / 2], zz[F / 4], wv[F / GPW];
 #pragma unroll
         for (int f = 0; f < F / 2; ++f) {
             const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(of[f]),
@@ -321,14 +329,28 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(z[f]),
                                                             __float_as_uint(z[f + F / 4]), false,
                                                             false);
-            wv[f] = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+            zz[f] = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+        }
+        if constexpr (GPW == 4) {
+#pragma unroll
+            for (int f = 0; f < F / 4; ++f) wv[f] = zz[f];
+        } else {
+            // lanes 0-7 of a row add register f of lanes 8-15, lanes 8-15 add
+            // register f+F/8 of lanes 0-7
+            const bool hi = (lane & 8) != 0;
+#pragma unroll
+            for (int f = 0; f < F / 8; ++f) {
+                const float t = hi ? zz[f] : zz[f + F / 8];
+                const float u = hi ? zz[f + F / 8] : zz[f];
+                wv[f] = u + dpp<0x128>(t);  // row_ror:8
+            }
         }
         __shared__ __align__(16) float s_ow[NW][GB * HD];
         __shared__ float s_mx[NW][GB];
         __shared__ float s_lw[NW][GB];
 #pragma unroll
-        for (int f = 0; f < F / 4; ++f) {
-            const int e = lg * (F / 4) + f;  // flat element of o held by this row
+        for (int f = 0; f < F / GPW; ++f) {
+            const int e = lg * (F / GPW) + f;  // flat element of o held by this lane group
             const int i = e / (NV * 4), v = (e / 4) % NV, c = e % 4;
             s_ow[wave][i * HD + 4 * (v * LPG + li) + c] = wv[f];
         }
