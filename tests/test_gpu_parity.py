@@ -136,6 +136,34 @@ def test_llama3_shape_prefill4096_continued_at_300():
             assert_close(g[b], om.attend(0, q[p], p), what=f"continued prefill row {p}")
 
 
+@pytest.mark.parametrize("start,n", [(0, 512), (0, 1000), (333, 700), (3000, 64), (40, 30),
+                                     (31, 2)])
+def test_llama3_shape_short_prefill_every_row(start, n):
+    # Llama-3-8B-shape prefills below the size that takes the DMA-staged
+    # kernel (the register-prefetch kernel, 16-row blocks of four heads),
+    # from the start of the cache and continued past it at tile-unaligned
+    # starts (a block's first rows then share their diagonal tile with the
+    # previous call's rows).  Every row against the oracle, K/V rows bit for
+    # bit.
+    dim, heads, kvh = 4096, 32, 8
+    rows = start + n
+    cfg = orc.Cfg(dim, heads, kvh, rows, 1, 5e5)
+    q = gen([94, start, n], (rows, dim))
+    k = gen([95, start, n], (rows, cfg.kv_dim))
+    v = gen([96, start, n], (rows, cfg.kv_dim))
+    om = orc.OracleModel(cfg)
+    with P.AttentionContext(dim, heads, kvh, rows, 1, 5e5) as ctx:
+        log(f"llama3 shape: prefill {n} rows at start {start}")
+        if start:
+            ctx.prefill(0, 0, q[:start], k[:start], v[:start])
+            om.append(0, 0, k[:start], v[:start])
+        g = ctx.prefill(0, start, q[start:], k[start:], v[start:])
+        ref = om.prefill(0, start, q[start:], k[start:], v[start:])
+        assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
+        assert_close(g, ref, what=f"prefill of {n} rows at {start}")
+
+
 def test_long_context_decode_131072():
     w = WORKLOADS["c5"]
     cfg = w.cfg()
