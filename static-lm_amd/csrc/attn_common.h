@@ -139,7 +139,10 @@ template <> struct LaneCfg<256> { static constexpr int LPG = 16; };
 // One online-softmax step of a lane group over TP positions (log2 domain):
 // scores q.k for GB heads reduced over the LPG lanes of the group, running
 // max m, running sum l, accumulator o (lazy rescale, see kLazyRescale).
-// Positions with valid[tp] false contribute nothing.
+// Positions with valid[tp] false contribute nothing.  m starts at -FLT_MAX,
+// not -inf: the first valid position then rescales by exp2(-FLT_MAX - mx) =
+// 0 like any other, and m - m and score - m never meet an infinite m, so the
+// exponents need no guard (two VALU instructions per head and position).
 template <int LPG, int NV, int GB, int TP>
 __device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
                                             const float4 (&kr)[TP][NV],
@@ -167,8 +170,7 @@ __device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
         for (int tp = 1; tp < TP; ++tp) mx = fmaxf(mx, sc[tp]);
         if (__any(mx > m[i] + kLazyRescale)) {  // wave-uniform
             const float mn = fmaxf(m[i], mx);
-            const float mu = (mn == -INFINITY) ? 0.0f : mn;
-            const float alpha = fast_exp2(m[i] - mu);
+            const float alpha = fast_exp2(m[i] - mn);
             l[i] *= alpha;
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
@@ -179,7 +181,7 @@ __device__ __forceinline__ void attend_tile(const float4 (&qr)[GB][NV],
             }
             m[i] = mn;
         }
-        const float mu = (m[i] == -INFINITY) ? 0.0f : m[i];
+        const float mu = m[i];
         float pr[TP];
         float ps = 0.0f;
 #pragma unroll

@@ -33,6 +33,7 @@
 // adds row p to its first lane group's state as one more position.  No other
 // workgroup reads row p.
 #include <hip/hip_ext.h>
+#include <float.h>
 #include <math.h>
 
 #include "attn_common.h"
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     float4 o[GB][NV];
 #pragma unroll
     for (int i = 0; i < GB; ++i) {
-        m[i] = -INFINITY;
+        m[i] = -FLT_MAX;  // finite: see attend_tile
         l[i] = 0.0f;
 #pragma unroll
         for (int v = 0; v < NV; ++v) o[i][v] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -297,13 +298,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         float mw[GB], lw[GB], of[F];
 #pragma unroll
         for (int i = 0; i < GB; ++i) {
-            // -inf when the wave saw no position
+            // -FLT_MAX when the wave saw no position
             if constexpr (GPW == 4)
                 mw[i] = rows_max(m[i]);
             else
                 mw[i] = groups_max<LPG>(m[i]);
-            const float mu = (mw[i] == -INFINITY) ? 0.0f : mw[i];
-            const float sc = fast_exp2(m[i] - mu);  // 0 for a lane group that saw nothing
+            // 0 for a lane group that saw nothing (its l and o are 0 anyway)
+            const float sc = fast_exp2(m[i] - mw[i]);
             if constexpr (GPW == 4)
                 lw[i] = rows_sum(l[i] * sc);
             else
@@ -368,11 +369,10 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             float mx = s_mx[0][i];
 #pragma unroll
             for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_mx[w][i]);
-            const float mu = (mx == -INFINITY) ? 0.0f : mx;
             float acc_o = 0.0f, acc_l = 0.0f;
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
-                const float e = fast_exp2(s_mx[w][i] - mu);  // 0 for a wave that saw nothing
+                const float e = fast_exp2(s_mx[w][i] - mx);  // 0 for a wave that saw nothing
                 acc_o += e * s_ow[w][idx];
                 acc_l += e * s_lw[w][i];
             }
@@ -409,7 +409,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             for (int i = 0; i < GB; ++i) s_mw[wave][i] = mg[i];
         }
         __syncthreads();
-        float mwg[GB];  // the workgroup max per head, 0 when no position was seen
+        float mwg[GB];  // the workgroup max per head, -FLT_MAX when no position was seen
 #pragma unroll
         for (int i = 0; i < GB; ++i) {
             float mx = s_mw[0][i];
@@ -420,8 +420,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         const int slot = wave * GPW + lg;
 #pragma unroll
         for (int i = 0; i < GB; ++i) {
-            const float mu = (mwg[i] == -INFINITY) ? 0.0f : mwg[i];
-            const float w = fast_exp2(m[i] - mu);  // 0 for a lane group that saw nothing
+            const float w = fast_exp2(m[i] - mwg[i]);  // 0 for a lane group that saw nothing
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
                 float4 x = o[i][v];
