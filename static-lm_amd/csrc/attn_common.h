@@ -124,18 +124,6 @@ __device__ __forceinline__ float wave_sum(float x) {
     return rows_sum(x);
 }
 
-// Lanes per position group for each compiled head_dim: every lane holds
-// head_dim / LPG floats (a multiple of 4, for 128-bit loads).
-template <int HD>
-struct LaneCfg;
-template <> struct LaneCfg<16> { static constexpr int LPG = 4; };
-template <> struct LaneCfg<32> { static constexpr int LPG = 8; };
-template <> struct LaneCfg<48> { static constexpr int LPG = 4; };
-template <> struct LaneCfg<64> { static constexpr int LPG = 8; };
-template <> struct LaneCfg<96> { static constexpr int LPG = 8; };
-template <> struct LaneCfg<128> { static constexpr int LPG = 8; };
-template <> struct LaneCfg<256> { static constexpr int LPG = 16; };
-
 // One online-softmax step of a lane group over TP positions (log2 domain):
 // scores q.k for GB heads reduced over the LPG lanes of the group, running
 // max m, running sum l, accumulator o (lazy rescale, see kLazyRescale).
@@ -232,13 +220,6 @@ __device__ __forceinline__ void lane_pair(float x, float& a, float& b) {
     }
 }
 
-// a*wa + b*wb with both products rounded before the add, so the two lanes of
-// a pair (which see the operands in opposite orders) get the same bits.
-__device__ __forceinline__ float pair_sum(float a, float wa, float b, float wb) {
-#pragma clang fp contract(off)
-    return a * wa + b * wb;
-}
-
 // Max over the lane groups of a wave (lanes with equal index inside their
 // LPG-lane group); every lane gets the result.
 template <int LPG>
@@ -264,50 +245,6 @@ __device__ __forceinline__ float groups_sum(float x) {
     } else {
         return x;
     }
-}
-
-// Merges the online-softmax states of lane groups OFF apart, then the next
-// level up to the whole wave.
-template <int OFF, int NV, int GB>
-__device__ __forceinline__ void merge_lane_round(float (&m)[GB], float (&l)[GB],
-                                                 float4 (&o)[GB][NV]) {
-    if constexpr (OFF < 64) {
-#pragma unroll
-        for (int i = 0; i < GB; ++i) {
-            float ma, mb, la, lb;
-            lane_pair<OFF>(m[i], ma, mb);
-            lane_pair<OFF>(l[i], la, lb);
-            const float mn = fmaxf(ma, mb);
-            const float mu = (mn == -INFINITY) ? 0.0f : mn;
-            const float wa = fast_exp2(ma - mu);
-            const float wb = fast_exp2(mb - mu);
-            l[i] = pair_sum(la, wa, lb, wb);
-#pragma unroll
-            for (int v = 0; v < NV; ++v) {
-                float4 x = o[i][v];
-                float xa, xb;
-                lane_pair<OFF>(x.x, xa, xb);
-                x.x = pair_sum(xa, wa, xb, wb);
-                lane_pair<OFF>(x.y, xa, xb);
-                x.y = pair_sum(xa, wa, xb, wb);
-                lane_pair<OFF>(x.z, xa, xb);
-                x.z = pair_sum(xa, wa, xb, wb);
-                lane_pair<OFF>(x.w, xa, xb);
-                x.w = pair_sum(xa, wa, xb, wb);
-                o[i][v] = x;
-            }
-            m[i] = mn;
-        }
-        merge_lane_round<2 * OFF, NV, GB>(m, l, o);
-    }
-}
-
-// Merges the states of the 64 / LPG lane groups of a wave; every lane ends
-// with the wave's state.
-template <int LPG, int NV, int GB>
-__device__ __forceinline__ void merge_lane_groups(float (&m)[GB], float (&l)[GB],
-                                                  float4 (&o)[GB][NV]) {
-    merge_lane_round<LPG, NV, GB>(m, l, o);
 }
 
 // Query heads that share one loaded K/V segment in a workgroup.
