@@ -143,11 +143,14 @@ def fill_cache(torch, ctx, layers: int, msl: int, rows: int, seed: int) -> None:
 
 
 def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768,
-                     steady_warmup: int = 0) -> dict:
+                     steady_warmup: int = 0, graph_reps: int = 0) -> dict:
     """Decode at position ctx_len - 1 through 8 layers of the Llama-3-8B head
     shape (KV caches of ctx_len rows each, rotated per step).  With
     steady_warmup > 0 the same steps are timed once more after that many
-    further untimed steps (the clock's steady state)."""
+    further untimed steps (the clock's steady state).  With graph_reps > 0
+    one step is also recorded as a HIP graph and replayed that many times
+    back to back (the GPU's time per step without the host's per-call cost;
+    every replay rewrites the same appended rows)."""
     layers = 8
     pos = ctx_len - 1
     ctx = P.AttentionContext(DIM, HEADS, KV_HEADS, ctx_len, layers, THETA)
@@ -213,6 +216,28 @@ def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768,
         steady = {"warmup_steps": warmup + steady_warmup, "steps": steps,
                   "ms_per_step": round(ms_s / steps, 5),
                   "gbs": round(step_bytes * steps / (ms_s / 1e3) / 1e9, 2)}
+    graph_us = None
+    if graph_reps > 0:
+        graph = None
+        try:
+            ctx.capture_begin()
+            try:
+                step()
+            finally:  # the stream leaves capture mode whatever happened
+                graph = ctx.capture_end()
+            for _ in range(3):
+                ctx.graph_launch(graph)
+            e0.record(stream)
+            for _ in range(graph_reps):
+                ctx.graph_launch(graph)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            graph_us = e0.elapsed_time(e1) / graph_reps / layers * 1e3
+        except P.SlmAttnError as exc:
+            log(f"decode @{ctx_len}: graph replay not measured: {exc}")
+        finally:
+            if graph is not None:
+                graph.close()
     ns, tile = ctx.decode_splits(pos + 1)
     finite = bool(torch.isfinite(out).all().item())
     # what the oracle needs to replay layer 0 of the timed configuration: its
@@ -229,7 +254,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768,
         "split_kernel_bytes": kv_bytes, "split_kernel_gbs": achieved,
         "splits": ns, "tile": tile, "finite": finite,
         "combine_avg_us": comb_ms / max(n_comb, 1) * 1e3,
-        "steady": steady,
+        "steady": steady, "graph_us_per_layer_step": graph_us,
         "_check": check,
     }
 
@@ -237,18 +262,26 @@ def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768,
 def bench_decode_short(torch, P, args) -> dict:
     """Decode steps back to back at 4096 and 600 cached rows (8 layers of the
     Llama-3-8B head shape): the latency-bound lengths of the C4 decode steps
-    and of a model decode after a 512-token prompt."""
+    and of a model decode after a 512-token prompt.  Launched one call at a
+    time from Python the host's cost per call is close to the GPU's per
+    step, so the same step is also replayed as a HIP graph."""
     short = {}
     for n_ctx in (4096, 600):
-        ds = bench_decode_32k(torch, P, max(20, args.steps), args.warmup, ctx_len=n_ctx)
+        ds = bench_decode_32k(torch, P, max(20, args.steps), args.warmup, ctx_len=n_ctx,
+                              graph_reps=100)
         us = ds["ms"] / ds["steps"] / ds["layers"] * 1e3
+        gus = ds["graph_us_per_layer_step"]
         short[f"ctx{n_ctx}"] = {
             "us_per_layer_step": round(us, 3), "gbs": round(ds["gbs"], 1),
             "frac_hbm": round(ds["gbs"] / HBM_PEAK_GBS, 4), "splits": ds["splits"],
             "decode_kernel_us_stamped": round(ds["split_kernel_avg_us"], 3),
             "combine_kernel_us_stamped": round(ds["combine_avg_us"], 3),
+            "us_per_layer_step_graph": round(gus, 3) if gus else None,
+            "gbs_graph": (round(ds["step_bytes"] / ds["layers"] / (gus / 1e6) / 1e9, 1)
+                          if gus else None),
         }
-        log(f"decode @{n_ctx}: {us:.2f} us per layer-step, {ds['gbs']:.0f} GB/s")
+        log(f"decode @{n_ctx}: {us:.2f} us per layer-step, {ds['gbs']:.0f} GB/s"
+            + (f"; replayed as a graph {gus:.2f} us" if gus else ""))
     return short
 
 
