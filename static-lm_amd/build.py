@@ -1,6 +1,7 @@
 """Builds libslm_attn.so (HIP, gfx950) in-tree with hipcc.
 
-Every HIP source is compiled with packed-fp32 ops disabled and no fast-math;
+Every HIP source is compiled with packed-fp32 ops disabled, no fast-math and
+warnings as errors;
 the RoPE/append kernels additionally switch FMA contraction off in source so
 that the KV rows they write are bit-identical to the reference's f32
 arithmetic.
@@ -38,6 +39,7 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Wall",
+    "-Werror",
     "-Wno-unused-result",
     # packed FP32 (v_pk_*_f32) is kept out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -33,6 +33,7 @@
 
 #include "attn_common.h"
 #include "slm_internal.h"
+#include "tile_range.h"
 
 namespace slm {
 namespace {
@@ -305,7 +306,9 @@ prefill_mfma_kernel(PrefillParams p) {
     };
     float4 pk[DMA ? 1 : NPF], pv[DMA ? 1 : NPF];
     auto prefetch = [&](int kb, int buf) __attribute__((always_inline)) {
-        const int bytes = (kv_len - kb) * p.kv_dim * 4;  // rows kb..kv_len-1
+        // rows kb .. min(kv_len, kb + kKT) - 1 (64-bit, clamped: the K slice
+        // of one layer may pass 4 GiB)
+        const int bytes = (int)tile_range_bytes(kv_len, kb, kKT, p.kv_dim);
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(kg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(

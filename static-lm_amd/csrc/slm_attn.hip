@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "slm_host.h"
+#include "tile_range.h"
 
 // Scratch of slm_attn_decode_xb_dev_noalloc: q | k | v rows of one token,
 // then the decode split partials.  Every device the library runs on holds
@@ -492,6 +493,10 @@ int slm_attn_create(const slm_attn_config* cfg, slm_attn_ctx** out) {
         return fail(nullptr, SLM_ERR_UNSUPPORTED,
                     "head_dim " + std::to_string(hd) +
                         " is not compiled (16, 32, 48, 64, 96, 128, 256)");
+    if ((long)hd * cfg->num_kv_heads > slm::kMaxKvDim)
+        return fail(nullptr, SLM_ERR_UNSUPPORTED,
+                    "kv_dim above " + std::to_string(slm::kMaxKvDim) +
+                        " is not supported (the kernels' per-thread tile offsets are 32-bit)");
 
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);

@@ -93,6 +93,58 @@ def test_create_rejects_uncompiled_head_dim():
     assert ei.value.code == P.ERR_UNSUPPORTED
 
 
+def test_create_rejects_kv_dim_past_the_tile_offset_limit():
+    # 65,600 KV heads of 16 dims: kv_dim 1,049,600 > 2^20, whose 32-row tile
+    # offsets the prefill kernels could not hold in 32 bits; refused before
+    # any device call
+    with pytest.raises(P.SlmAttnError) as ei:
+        P.AttentionContext(16 * 65600, 65600, 65600, 4, 1)
+    assert ei.value.code == P.ERR_UNSUPPORTED
+    assert "kv_dim" in ei.value.message
+
+
+TILE_RANGE_PROBE = r"""
+#include <stdio.h>
+#include "tile_range.h"
+int main(void) {
+    static const int cases[][4] = {
+        /* kv_len, kb, tile_rows, kv_dim */
+        {1048600, 0, 32, 1024},     /* one layer's K slice past 4 GiB: the first tile */
+        {1048600, 1048576, 32, 1024},  /* the tile at row 2^20: 24 rows left */
+        {1048600, 1048576 + 8, 32, 1024},  /* 16 rows left */
+        {262144, 0, 32, 4096},      /* hd-128 MHA, 262,144 rows: 4 GiB per slice */
+        {2147483647, 0, 32, 1 << 20},  /* the largest kv_dim a context accepts */
+        {100, 100, 32, 1024},       /* no rows left */
+        {100, 120, 32, 1024},       /* past the end */
+        {2147483647, 0, 2147483647, 1 << 20},  /* an untiled range: clamped to 32 bits */
+    };
+    for (unsigned i = 0; i < sizeof(cases) / sizeof(cases[0]); ++i)
+        printf("%u\n", slm::tile_range_bytes(cases[i][0], cases[i][1], cases[i][2], cases[i][3]));
+    return 0;
+}
+"""
+
+
+def test_prefill_tile_range_is_64_bit_and_clamped_to_the_tile(tmp_path):
+    """The prefill kernels' buffer-descriptor range (csrc/tile_range.h),
+    compiled for the host: a layer slice past 4 GiB (1,048,600 rows of 1024
+    floats) must still give whole 32-row tiles, where the 32-bit product
+    (kv_len - kb) * kv_dim * 4 wrapped to 24 rows for the first tile."""
+    src = tmp_path / "probe.cpp"
+    src.write_text(TILE_RANGE_PROBE)
+    exe = tmp_path / "probe"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror",
+                    f"-I{P.PKG_DIR / 'csrc'}", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    row = 1024 * 4
+    assert got == [32 * row, 24 * row, 16 * row, 32 * 4096 * 4, 32 * (1 << 20) * 4, 0, 0,
+                   0xFFFFFFFF]
+    # what the old 32-bit product gave for the first case: the wrap the
+    # clamp removes
+    assert (1048600 * 1024 * 4) % (1 << 32) == 24 * row
+
+
 def test_header_declares_error_codes_the_binding_uses():
     text = "".join(h.read_text() for h in (P.HEADER_PATH, P.QUANT_HEADER_PATH,
                                              P.LAYER_HEADER_PATH, P.GGUF_HEADER_PATH))

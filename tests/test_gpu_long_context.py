@@ -41,21 +41,21 @@ def log(msg):
     sys.stdout.flush()
 
 
-def v_int_rows(p0: int, n: int, kv_dim: int = KV_DIM) -> np.ndarray:
-    """V rows p0..p0+n-1: integers 0..60 that depend on the row, its 32-row
-    tile and the column."""
+def v_int_rows(p0: int, n: int, kv_dim: int = KV_DIM, mod: int = 61) -> np.ndarray:
+    """V rows p0..p0+n-1: integers 0..mod-1 that depend on the row, its
+    32-row tile and the column."""
     t = np.arange(p0, p0 + n, dtype=np.int64)[:, None]
     d = np.arange(kv_dim, dtype=np.int64)[None, :]
-    return (t * 7 + d * 13 + (t // 32) * 5) % 61
+    return (t * 7 + d * 13 + (t // 32) * 5) % mod
 
 
-def v_int_rows_dev(p0: int, n: int, kv_dim: int = KV_DIM):
+def v_int_rows_dev(p0: int, n: int, kv_dim: int = KV_DIM, mod: int = 61):
     t = torch.arange(p0, p0 + n, device="cuda", dtype=torch.int64)[:, None]
     d = torch.arange(kv_dim, device="cuda", dtype=torch.int64)[None, :]
-    return ((t * 7 + d * 13 + torch.div(t, 32, rounding_mode="floor") * 5) % 61).to(torch.float32)
+    return ((t * 7 + d * 13 + torch.div(t, 32, rounding_mode="floor") * 5) % mod).to(torch.float32)
 
 
-def prefix_sums(p_list, kv_dim: int = KV_DIM) -> dict:
+def prefix_sums(p_list, kv_dim: int = KV_DIM, mod: int = 61) -> dict:
     """Exact sum over rows 0..p of v_int_rows for each p in p_list (int64)."""
     out = {}
     acc = np.zeros(kv_dim, np.int64)
@@ -64,7 +64,7 @@ def prefix_sums(p_list, kv_dim: int = KV_DIM) -> dict:
     for p in sorted(p_list):
         while done <= p:
             n = min(blk, p + 1 - done)
-            acc += v_int_rows(done, n, kv_dim).sum(axis=0)
+            acc += v_int_rows(done, n, kv_dim, mod).sum(axis=0)
             done += n
         out[p] = acc.copy()
     return out
@@ -87,10 +87,10 @@ def check(got, want, what):
     assert float(rel.max()) <= REL_BAR, f"{what}: max-rel {float(rel.max()):.3e} > {REL_BAR}"
 
 
-def fill_v(ctx, layer: int, rows: int, blk: int = 16384):
+def fill_v(ctx, layer: int, rows: int, blk: int = 16384, mod: int = 61):
     for p0 in range(0, rows, blk):
         n = min(blk, rows - p0)
-        v = v_int_rows_dev(p0, n)
+        v = v_int_rows_dev(p0, n, mod=mod)
         ctx.kv_write_dev(layer, 1, p0, n, v.data_ptr())
     ctx.sync()
 
@@ -178,3 +178,85 @@ def test_prefill_uniform_scores_every_row(start, n):
             / (rows + 1)[:, None, None].astype(np.float64))
     want = np.repeat(want, kv_mul, axis=1).reshape(n, DIM)
     check(got, want, f"prefill rows {start}..{total - 1}")
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads,start,n", [
+    (4096, 32, 8, 7, 4111),   # 129 query blocks of 32: the last holds 15 rows, so its
+                              # second 16-row wave has none but joins every DMA and barrier
+    (8192, 64, 8, 0, 2100),   # kv_mul 8: two workgroups' head groups share each KV head
+])
+def test_dma_prefill_unaligned_every_row(dim, heads, kv_heads, start, n):
+    """Zero keys through the DMA-fed prefill kernel (hd 128, four query heads
+    per workgroup, at least four workgroups per CU on 256 CUs) at row counts
+    that are not multiples of its 32-row query block: every row against the
+    closed form."""
+    hd = dim // heads
+    kv_dim = hd * kv_heads
+    total = start + n
+    v_all = v_int_rows(0, total, kv_dim)
+    cums = np.cumsum(v_all, axis=0)
+    log(f"DMA prefill {heads}/{kv_heads} heads, rows {start}..{total - 1}")
+    with P.AttentionContext(dim, heads, kv_heads, total, 1, 5e5) as ctx:
+        q = torch.from_numpy(gen([23, start], (total, dim))).cuda()
+        k = torch.zeros(total, kv_dim, device="cuda")
+        v = torch.from_numpy(v_all.astype(np.float32)).cuda()
+        out = torch.empty(total, dim, device="cuda")
+        if start:
+            ctx.prefill_dev(0, 0, start, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                            out.data_ptr())
+        ctx.prefill_dev(0, start, n, q[start:].data_ptr(), k[start:].data_ptr(),
+                        v[start:].data_ptr(), out[start:].data_ptr())
+        ctx.sync()
+        got = out[start:].cpu().numpy().astype(np.float64)
+    rows = np.arange(start, total)
+    want = (cums[rows].reshape(n, kv_heads, hd).astype(np.float64)
+            / (rows + 1)[:, None, None].astype(np.float64))
+    want = np.repeat(want, heads // kv_heads, axis=1).reshape(n, dim)
+    check(got, want, f"DMA prefill rows {start}..{total - 1}")
+
+def test_prefill_and_decode_past_row_2_pow_20():
+    """One layer's K slice past 4 GiB (1,048,600 rows of kv_dim 1024, an
+    8.6 GB cache): zero keys and V integers 0..15 (every sum below 2^24
+    stays exact).  The 32-row prefill takes the register-prefetch kernel,
+    the 4096-row one the DMA kernel; both end at row 1,048,599, so their
+    first tiles' buffer ranges would have wrapped in 32 bits (to 8 and 24
+    rows), reading the other rows of those tiles as zeros.  Every row of
+    both against the closed form, then one decode at the last position."""
+    msl = (1 << 20) + 24
+    mod = 16
+    log(f"past 2^20: msl {msl}, KV {2 * msl * KV_DIM * 4 / 1e9:.1f} GB")
+    last = msl - 1
+    n_big = 4096
+    s_big = msl - n_big
+    base = prefix_sums([s_big - 1], mod=mod)[s_big - 1]
+    tail = v_int_rows(s_big, n_big, mod=mod)
+    cums = base[None, :] + np.cumsum(tail, axis=0)  # exact sums over rows 0..s_big+b
+    kv_mul = HEADS // KV_HEADS
+
+    def want_rows(b0, n):
+        rows = np.arange(b0, b0 + n)  # positions
+        s = cums[rows - s_big].reshape(n, KV_HEADS, HD).astype(np.float64)
+        w = s / (rows + 1)[:, None, None].astype(np.float64)
+        return np.repeat(w, kv_mul, axis=1).reshape(n, DIM)
+
+    with P.AttentionContext(DIM, HEADS, KV_HEADS, msl, 1, 5e5) as ctx:
+        fill_v(ctx, 0, msl, mod=mod)  # K rows stay zero
+        for n in (32, n_big):
+            start = msl - n
+            log(f"past 2^20: prefill {n} rows at {start}")
+            q = torch.from_numpy(gen([31, n], (n, DIM))).cuda()
+            k = torch.zeros(n, KV_DIM, device="cuda")
+            v = v_int_rows_dev(start, n, mod=mod).contiguous()
+            out = torch.empty(n, DIM, device="cuda")
+            ctx.prefill_dev(0, start, n, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                            out.data_ptr())
+            ctx.sync()
+            check(out.cpu().numpy(), want_rows(start, n), f"prefill rows {start}..{last}")
+        log(f"past 2^20: decode at {last}")
+        q = torch.from_numpy(gen([32, last], DIM)).cuda()
+        knew = torch.zeros(KV_DIM, device="cuda")
+        vrow = v_int_rows_dev(last, 1, mod=mod)[0].contiguous()
+        out = torch.empty(DIM, device="cuda")
+        ctx.decode_dev(0, last, q.data_ptr(), knew.data_ptr(), vrow.data_ptr(), out.data_ptr())
+        ctx.sync()
+        check(out.cpu().numpy(), want_rows(last, 1)[0], f"decode pos {last}")

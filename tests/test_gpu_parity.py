@@ -136,6 +136,35 @@ def test_llama3_shape_prefill4096_continued_at_300():
             assert_close(g[b], om.attend(0, q[p], p), what=f"continued prefill row {p}")
 
 
+@pytest.mark.parametrize("dim,heads,kv_heads,start,n", [(4096, 32, 8, 7, 4111),
+                                                        (8192, 64, 8, 0, 2100)])
+def test_dma_prefill_unaligned_against_oracle(dim, heads, kv_heads, start, n):
+    # The DMA-staged prefill kernel at row counts that leave a partial last
+    # 32-row query block (4111 rows: 15 in the last block, whose second wave
+    # has none) and with two head groups per KV head (kv_mul 8).  K/V rows bit
+    # for bit; rows around the block edges and the last rows against the
+    # oracle over the same cache.
+    w = Workload("dma-unaligned", dim, heads, kv_heads, start + n, 1, 5e5, n, 0)
+    cfg = w.cfg()
+    rows = start + n
+    q = gen([94, dim], (rows, dim))
+    k = gen([95, dim], (rows, w.kv_dim))
+    v = gen([96, dim], (rows, w.kv_dim))
+    with make_ctx(w) as ctx:
+        log(f"DMA prefill {heads}/{kv_heads} heads: {n} rows at start {start}")
+        if start:
+            ctx.prefill(0, 0, q[:start], k[:start], v[:start])
+        g = ctx.prefill(0, start, q[start:], k[start:], v[start:])
+        om = orc.OracleModel(cfg)
+        om.append(0, 0, k, v)
+        assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
+        for b in (0, 1, 15, 16, 31, 32, 33, 1000, n - 33, n - 21, n - 20, n - 17, n - 16,
+                  n - 15, n - 2, n - 1):
+            p = start + b
+            assert_close(g[b], om.attend(0, q[p], p), what=f"DMA prefill row {p}")
+
+
 @pytest.mark.parametrize("start,n", [(0, 512), (0, 1000), (333, 700), (3000, 64), (40, 30),
                                      (31, 2)])
 def test_llama3_shape_short_prefill_every_row(start, n):
