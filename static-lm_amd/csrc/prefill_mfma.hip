@@ -305,9 +305,10 @@ prefill_mfma_kernel(PrefillParams p) {
                            __uint_as_float(x.w));
     };
     float4 pk[DMA ? 1 : NPF], pv[DMA ? 1 : NPF];
+    static_assert(tile_range_fits(kKT, kMaxKvDim), "tile ranges must fit 32 bits");
     auto prefetch = [&](int kb, int buf) __attribute__((always_inline)) {
-        // rows kb .. min(kv_len, kb + kKT) - 1 (64-bit, clamped: the K slice
-        // of one layer may pass 4 GiB)
+        // rows kb .. min(kv_len, kb + kKT) - 1: bounded by the tile (one
+        // layer's K slice may pass 4 GiB)
         const int bytes = (int)tile_range_bytes(kv_len, kb, kKT, p.kv_dim);
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(kg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
