@@ -111,9 +111,10 @@ int slm_model_prefill_dev(slm_attn_ctx* ctx, const slm_model_weights* w, float r
  * and stopping after `eos` (eos < 0: none) or at max_seq_len.  *n_out is the
  * number written (0 for an empty prompt or max_out == 0).  The decode steps
  * are pipelined (each token is read back while the next step runs on the
- * device), so when generation stops at `eos` one more step has run and been
- * discarded: the K/V row at the position after the last returned token is
- * written, which the reference leaves untouched. */
+ * device); when generation stops at `eos` the step already run on the EOS
+ * token is discarded and the K/V rows it wrote (every layer, at the position
+ * after the last returned token) are restored, so the cache holds exactly
+ * what the reference's leaves: rows 0..n_prompt + *n_out - 2 written. */
 int slm_model_generate_dev(slm_attn_ctx* ctx, const slm_model_weights* w, float rms_eps,
                            const int32_t* prompt, int32_t n_prompt, int32_t* out_tokens,
                            int32_t max_out, int32_t eos, int32_t* n_out);

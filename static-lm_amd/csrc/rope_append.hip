@@ -49,7 +49,30 @@ __global__ __launch_bounds__(256) void rope_kernel(
     row[p] = rope_pair_exact(row[p], cos_t[pos * half + j], sin_t[pos * half + j]);
 }
 
+// Row pos of each of the rows K/V slices (kv_row points at row pos of the
+// first; the slices are pitch floats apart) to or from packed [rows][kv_dim].
+__global__ __launch_bounds__(256) void kv_rows_copy_kernel(float* __restrict__ kv_row,
+                                                           float* __restrict__ packed, long pitch,
+                                                           int kv_dim4, bool to_packed) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= kv_dim4) return;
+    float4* a = reinterpret_cast<float4*>(kv_row + blockIdx.y * pitch) + i;
+    float4* b = reinterpret_cast<float4*>(packed) + (long)blockIdx.y * kv_dim4 + i;
+    if (to_packed)
+        *b = *a;
+    else
+        *a = *b;
+}
+
 }  // namespace
+
+hipError_t launch_kv_rows_copy(const Shape& s, float* kv_row, float* packed, int rows,
+                               bool to_packed, hipStream_t st) {
+    const int kv_dim4 = s.kv_dim / 4;
+    hipLaunchKernelGGL(kv_rows_copy_kernel, dim3((kv_dim4 + 255) / 256, rows), dim3(256), 0, st,
+                       kv_row, packed, (long)s.max_seq_len * s.kv_dim, kv_dim4, to_packed);
+    return hipGetLastError();
+}
 
 // Rows per launch so that the 32-bit thread index cannot overflow.
 static int rows_per_launch(int row_len) {

@@ -616,6 +616,7 @@ void slm_attn_destroy(slm_attn_ctx* c) {
     (void)hipFree(c->mdl_logits);
     (void)hipFree(c->mdl_flags);
     (void)hipFree(c->mdl_parts);
+    (void)hipFree(c->gen_rows);
     if (c->tok_pin) (void)hipHostFree(c->tok_pin);
     for (hipEvent_t e : c->tok_ev)
         if (e) (void)hipEventDestroy(e);

@@ -85,6 +85,10 @@ struct slm_attn_ctx {
     size_t mdl_parts_n = 0;
     int32_t* tok_pin = nullptr;            // pinned [2]: generate's tokens, read back
     hipEvent_t tok_ev[2] = {nullptr, nullptr};  // one step behind the device
+    // generate's copy of the K and V rows of every layer at the position a
+    // step launched ahead of its previous token writes ([2 * layers][kv_dim])
+    float* gen_rows = nullptr;
+    size_t gen_rows_floats = 0;
     // the stream is being captured into a HIP graph (slm_attn_capture_begin)
     bool capturing = false;
     // kernel timing

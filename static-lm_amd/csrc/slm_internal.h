@@ -27,6 +27,12 @@ hipError_t launch_kv_append(const Shape& s, const float* k, const float* v,
                             const float* sin_t, int pos0, int n,
                             hipStream_t st);
 
+// Row pos of `rows` consecutive K/V slices ([layer][K|V][msl][kv_dim]; kv_row
+// points at row pos of the first) to (to_packed) or from packed
+// [rows][kv_dim].
+hipError_t launch_kv_rows_copy(const Shape& s, float* kv_row, float* packed, int rows,
+                               bool to_packed, hipStream_t st);
+
 // In-place apply_rope_cached on n rows of row_len floats at pos0..pos0+n-1.
 hipError_t launch_rope(const Shape& s, float* x, int n, int row_len, int pos0,
                        const float* cos_t, const float* sin_t, hipStream_t st);

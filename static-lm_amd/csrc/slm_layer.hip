@@ -378,6 +378,17 @@ int ensure_token_readback(slm_attn_ctx* c) {
     return SLM_OK;
 }
 
+// The K and V rows at `pos` of layers 0..layers-1 to (save) or from
+// (restore) gen_rows: in the [layer][K|V][msl][kv_dim] region those 2 * layers
+// rows are msl * kv_dim floats apart, one launch.
+int gen_rows_copy(slm_attn_ctx* c, int pos, int layers, bool save) {
+    Timed t(c, SLM_K_ELEM);
+    hipError_t e = slm::launch_kv_rows_copy(c->shape, c->kv + (size_t)pos * c->shape.kv_dim,
+                                            c->gen_rows, 2 * layers, save, c->stream);
+    t.done();
+    return launch_status(c, e, "K/V row copy kernel launch");
+}
+
 int model_prefill(slm_attn_ctx* c, const slm_model_weights* w, float eps, const int32_t* tokens,
                   int n, int start, float* logits, int32_t* next) {
     int rc, vocab = 0;
@@ -435,14 +446,26 @@ int slm_model_generate_dev(slm_attn_ctx* c, const slm_model_weights* w, float rm
         return SLM_OK;
     }
     // Greedy decode (:867-897), pipelined: step k's token is read on the host
-    // while step k + 1 already runs, so the device never waits for the host;
-    // a step launched after the EOS token is drained and its token dropped
-    // (its K/V row, one past the returned sequence, is written).
+    // while step k + 1 already runs, so the device never waits for the host.
+    // When step k's token is EOS, step k + 1 has already run on it, which the
+    // reference never does (it stops before forward_token of the EOS token):
+    // that step's token is dropped, and the K/V rows it wrote at position
+    // n_prompt + k + 1 are put back from the copy taken before it ran, so the
+    // cache ends exactly as the reference leaves it.  (Without an EOS id no
+    // step runs ahead of a stop, and no copies are made.)
     const int steps = std::min(max_out - 1, c->cfg.max_seq_len - n_prompt);
     int vocab = 0;
     if ((rc = check_model(c, w, &vocab)) || (rc = ensure_token_readback(c))) return rc;
+    const bool may_stop = eos >= 0;
+    if (may_stop && (rc = ensure_buffer(c, &c->gen_rows, &c->gen_rows_floats,
+                                        (size_t)2 * w->num_layers * c->shape.kv_dim,
+                                        "hipMalloc(generate's K/V rows)")))
+        return rc;
     for (int k = 0; k <= steps; ++k) {
-        if (k < steps && (rc = decode_step(c, w, rms_eps, n_prompt + k, vocab, k & 1))) {
+        // step 0 follows the prompt's token, already known not to be EOS
+        if (k < steps && ((k > 0 && may_stop &&
+                           (rc = gen_rows_copy(c, n_prompt + k, w->num_layers, true))) ||
+                          (rc = decode_step(c, w, rms_eps, n_prompt + k, vocab, k & 1)))) {
             (void)hipStreamSynchronize(c->stream);
             *n_out = generated;
             return rc;
@@ -451,7 +474,14 @@ int slm_model_generate_dev(slm_attn_ctx* c, const slm_model_weights* w, float rm
         SLM_HIP(c, hipEventSynchronize(c->tok_ev[(k - 1) & 1]));
         next = c->tok_pin[(k - 1) & 1];
         out_tokens[generated++] = next;
-        if (eos >= 0 && next == eos) break;
+        if (may_stop && next == eos) {
+            if (k < steps && (rc = gen_rows_copy(c, n_prompt + k, w->num_layers, false))) {
+                (void)hipStreamSynchronize(c->stream);
+                *n_out = generated;
+                return rc;
+            }
+            break;
+        }
     }
     SLM_HIP(c, hipStreamSynchronize(c->stream));
     *n_out = generated;

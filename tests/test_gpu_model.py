@@ -130,6 +130,81 @@ def test_generate_stops_at_eos_and_max_seq_len():
         dm.close()
 
 
+def kv_snapshot(c, cfg, layers):
+    return np.stack([c.kv_read(l, which, 0, cfg.max_seq_len)
+                     for l in range(layers) for which in (0, 1)])
+
+
+def sentinel_fill(c, cfg, layers):
+    # rows no call has written keep these values, distinct per layer and side
+    for l in range(layers):
+        for which in (0, 1):
+            rows = np.full((cfg.max_seq_len, cfg.kv_dim), -3.25 - l - 0.5 * which, np.float32)
+            c.kv_write(l, which, 0, rows)
+
+
+@pytest.mark.parametrize("stop", ["second", "middle", "last"])
+def test_generate_eos_leaves_the_cache_as_the_reference(stop):
+    """generate stops after forward_token produced EOS and never runs it on
+    the EOS token (transformer.rs:874-889).  The device pipelines its decode
+    steps, so one step has already run on the EOS token when the host sees
+    it; the K/V rows that step wrote must be put back.  The whole cache after
+    generate (every layer, K and V, every row, over a sentinel fill) must
+    equal bit for bit the cache after prefill + forward_token of each
+    returned token but the last, and the row after the returned sequence must
+    keep the sentinel.  Tokens against the oracle's generate with the same
+    EOS."""
+    cfg, w = ref_model()
+    layers = 2
+    prompt = [5, 6]
+    dm = DeviceModel(cfg, w)
+    try:
+        def ctx():
+            return P.AttentionContext(cfg.dim, cfg.num_heads, cfg.num_kv_heads,
+                                      cfg.max_seq_len, layers, 1e4)
+        with ctx() as c:
+            full = c.model_generate_dev(dm.w, EPS, prompt, 40)
+        i = {"second": 1, "middle": len(full) // 2, "last": len(full) - 1}[stop]
+        eos = full[i]
+        want_tokens = full[:full.index(eos) + 1]
+        log(f"full run {full}; EOS {eos} -> {want_tokens}")
+        with ctx() as a:
+            sentinel_fill(a, cfg, layers)
+            before = kv_snapshot(a, cfg, layers)
+            out = a.model_generate_dev(dm.w, EPS, prompt, 40, eos=eos)
+            got = kv_snapshot(a, cfg, layers)
+        assert out == want_tokens
+        # the oracle on the same tokens: each step's argmax wherever its top
+        # two logits are clearly apart, logits within the bound
+        om = orc.OracleModel(cfg)
+        feed = [(prompt, 0)] + [([out[j - 1]], len(prompt) + j - 1) for j in range(1, len(out))]
+        for j, (toks, pos) in enumerate(feed):
+            want, onext, _ = orc.model_forward(om, w, EPS, toks, pos)
+            if clear_winner(want):
+                assert onext == out[j], (j, onext, out[j])
+        log(f"generate with EOS {out}: oracle argmax agrees")
+        with ctx() as b:
+            sentinel_fill(b, cfg, layers)
+            nxt = b.model_prefill_dev(dm.w, EPS, prompt)
+            assert nxt == out[0]
+            for j in range(1, len(out)):
+                nxt = b.model_forward_token_dev(dm.w, EPS, out[j - 1], len(prompt) + j - 1)
+                assert nxt == out[j]
+            b.sync()
+            seq = kv_snapshot(b, cfg, layers)
+        assert_kv_equal(got, seq, "generate with EOS against prefill + forward_token")
+        last = len(prompt) + len(out) - 1  # the first row the reference leaves untouched
+        assert_kv_equal(got[:, last:], before[:, last:], f"rows {last}.. keep their contents")
+        assert not np.array_equal(got[:, last - 1], before[:, last - 1])
+    finally:
+        dm.close()
+
+
+def assert_kv_equal(a, b, what):
+    neq = a.view(np.uint32) != b.view(np.uint32)
+    assert not neq.any(), f"{what}: {int(neq.sum())} of {neq.size} words differ"
+
+
 def test_embedding_against_oracle():
     cfg, w = ref_model()
     dm = DeviceModel(cfg, w)
