@@ -16,6 +16,7 @@ from __future__ import annotations
 import ctypes
 import os
 import sys
+import weakref
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -296,10 +297,13 @@ class AttentionContext:
         if rc != SLM_OK:
             raise SlmAttnError(rc, self.lib.slm_attn_last_error(None).decode())
         self._h = h
+        self._graphs = weakref.WeakSet()  # live recordings, closed before the context
 
     # -- lifetime -------------------------------------------------------------
     def close(self) -> None:
         if getattr(self, "_h", None):
+            for g in list(getattr(self, "_graphs", ())):
+                g.close()
             self.lib.slm_attn_destroy(self._h)
             self._h = None
 
@@ -473,7 +477,9 @@ class AttentionContext:
     def capture_end(self) -> "AttentionGraph":
         g = _P()
         self._check(self.lib.slm_attn_capture_end(self._h, ctypes.byref(g)))
-        return AttentionGraph(self.lib, g)
+        graph = AttentionGraph(self, g)
+        self._graphs.add(graph)
+        return graph
 
     def graph_launch(self, graph: "AttentionGraph") -> None:
         """Replays a recording on the context stream (asynchronous)."""
@@ -522,10 +528,14 @@ class AttentionContext:
 
 
 class AttentionGraph:
-    """A recording of device-pointer calls (slm_attn_capture_end)."""
+    """A recording of device-pointer calls (slm_attn_capture_end).  It keeps
+    its context alive, and is destroyed as slm_attn.h asks: after its replays
+    have finished (the context's stream is synchronized first) and before the
+    context (AttentionContext.close closes its live graphs)."""
 
-    def __init__(self, lib, handle):
-        self.lib = lib
+    def __init__(self, ctx: "AttentionContext", handle):
+        self.lib = ctx.lib
+        self._ctx = ctx
         self._h = handle
 
     @property
@@ -534,6 +544,12 @@ class AttentionGraph:
 
     def close(self) -> None:
         if getattr(self, "_h", None):
+            ctx = self._ctx
+            if ctx.handle:
+                rc = self.lib.slm_attn_sync(ctx.handle)
+                if rc != SLM_OK:
+                    raise SlmAttnError(rc, "graph not destroyed: " +
+                                       self.lib.slm_attn_last_error(ctx.handle).decode())
             self.lib.slm_attn_graph_destroy(self._h)
             self._h = None
 

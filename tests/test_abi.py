@@ -115,17 +115,18 @@ int main(void) {
         {262144, 0, 32, 4096},      /* hd-128 MHA, 262,144 rows: 4 GiB per slice */
         {2147483647, 0, 32, 1 << 20},  /* the largest kv_dim a context accepts */
         {100, 100, 32, 1024},       /* no rows left */
-        {100, 120, 32, 1024},       /* past the end */
-        {2147483647, 0, 2147483647, 1 << 20},  /* an untiled range: clamped to 32 bits */
+        {2147483647, 2147483647 - 5, 32, 1 << 20},  /* 5 rows left at the largest position */
     };
     for (unsigned i = 0; i < sizeof(cases) / sizeof(cases[0]); ++i)
         printf("%u\n", slm::tile_range_bytes(cases[i][0], cases[i][1], cases[i][2], cases[i][3]));
+    printf("%d %d\n", (int)slm::tile_range_fits(32, slm::kMaxKvDim),
+           (int)slm::tile_range_fits(1 << 11, 1 << 20));
     return 0;
 }
 """
 
 
-def test_prefill_tile_range_is_64_bit_and_clamped_to_the_tile(tmp_path):
+def test_prefill_tile_range_is_bounded_by_the_tile(tmp_path):
     """The prefill kernels' buffer-descriptor range (csrc/tile_range.h),
     compiled for the host: a layer slice past 4 GiB (1,048,600 rows of 1024
     floats) must still give whole 32-row tiles, where the 32-bit product
@@ -138,8 +139,11 @@ def test_prefill_tile_range_is_64_bit_and_clamped_to_the_tile(tmp_path):
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
                                           check=True).stdout.split()]
     row = 1024 * 4
-    assert got == [32 * row, 24 * row, 16 * row, 32 * 4096 * 4, 32 * (1 << 20) * 4, 0, 0,
-                   0xFFFFFFFF]
+    assert got[:7] == [32 * row, 24 * row, 16 * row, 32 * 4096 * 4, 32 * (1 << 20) * 4, 0,
+                       5 * (1 << 20) * 4]
+    # the kernels' 32-row tiles at the largest kv_dim a context accepts fit
+    # 32 bits; 2048-row tiles at that kv_dim would not
+    assert got[7:] == [1, 0]
     # what the old 32-bit product gave for the first case: the wrap the
     # clamp removes
     assert (1048600 * 1024 * 4) % (1 << 32) == 24 * row
@@ -150,3 +154,69 @@ def test_header_declares_error_codes_the_binding_uses():
                                              P.LAYER_HEADER_PATH, P.GGUF_HEADER_PATH))
     for code, name in P.ERRORS.items():
         assert f"#define {name} ({code})" in text
+
+
+class _RecordingLib:
+    """Stands in for the library: records the calls a graph's lifetime makes."""
+
+    def __init__(self):
+        self.calls = []
+
+    def slm_attn_sync(self, h):
+        self.calls.append(("sync", h))
+        return P.SLM_OK
+
+    def slm_attn_graph_destroy(self, g):
+        self.calls.append(("graph_destroy", g))
+
+    def slm_attn_destroy(self, h):
+        self.calls.append(("destroy", h))
+
+    def slm_attn_last_error(self, h):
+        return b""
+
+
+def _fake_context(lib):
+    ctx = P.AttentionContext.__new__(P.AttentionContext)
+    ctx.lib = lib
+    ctx._h = "ctx"
+    ctx._graphs = P.weakref.WeakSet()
+    return ctx
+
+
+def test_graph_is_destroyed_after_a_sync_and_before_its_context():
+    # slm_attn.h: destroy a graph only after its replays have finished, and
+    # before its context
+    lib = _RecordingLib()
+    ctx = _fake_context(lib)
+    g = P.AttentionGraph(ctx, "g1")
+    ctx._graphs.add(g)
+    g.close()
+    g.close()  # no-op
+    assert lib.calls == [("sync", "ctx"), ("graph_destroy", "g1")]
+    # a live graph is closed by its context, ahead of the context itself
+    lib.calls.clear()
+    g2 = P.AttentionGraph(ctx, "g2")
+    ctx._graphs.add(g2)
+    ctx.close()
+    assert lib.calls == [("sync", "ctx"), ("graph_destroy", "g2"), ("destroy", "ctx")]
+    lib.calls.clear()
+    g2.close()
+    del g2
+    assert lib.calls == []
+
+
+def test_temporary_graph_keeps_its_context_alive():
+    # a graph dropped without close() (e.g. ctx.graph_launch(ctx.capture_end()))
+    # still syncs before destroying, because it holds its context
+    import gc
+    lib = _RecordingLib()
+    ctx = _fake_context(lib)
+    g = P.AttentionGraph(ctx, "g3")
+    ctx._graphs.add(g)
+    del ctx
+    gc.collect()
+    assert lib.calls == []  # the graph holds the context
+    del g
+    gc.collect()
+    assert lib.calls[:2] == [("sync", "ctx"), ("graph_destroy", "g3")]
