@@ -69,7 +69,9 @@ int check_q4(const slm_gguf* g, const std::string& name) {
 }
 
 // Every tensor the upload reads, checked before any device work: present,
-// of the right type and, for the norm vectors, dim floats long.
+// of the right type and, for the norm vectors, dim floats long.  In the order
+// model_weights and layer_weights resolve them (loader.rs:508-552), so a file
+// with several faults gets the error of the first one the reference meets.
 int check_model_file(const slm_gguf* g, int num_layers, uint64_t dim) {
     int rc;
     if ((rc = check_q4(g, "token_embd.weight")) ||
@@ -79,15 +81,20 @@ int check_model_file(const slm_gguf* g, int num_layers, uint64_t dim) {
     if (slm_gguf_tensor_info(g, "output.weight", &out_info) == SLM_OK &&
         (rc = check_q4(g, "output.weight")))
         return rc;
-    static const char* const q4_names[] = {"attn_q", "attn_k", "attn_v", "attn_output",
-                                           "ffn_gate", "ffn_up", "ffn_down"};
+    // per layer: attn_norm, attn_q, attn_k, attn_v, attn_output, ffn_norm,
+    // ffn_gate, ffn_up, ffn_down (the norms f32, the rest Q4_0)
+    static const struct {
+        const char* name;
+        bool norm;
+    } tensors[] = {{"attn_norm", true}, {"attn_q", false},   {"attn_k", false},
+                   {"attn_v", false},   {"attn_output", false}, {"ffn_norm", true},
+                   {"ffn_gate", false}, {"ffn_up", false},   {"ffn_down", false}};
     for (int l = 0; l < num_layers; ++l) {
         const std::string p = "blk." + std::to_string(l) + ".";
-        if ((rc = check_f32(g, p + "attn_norm.weight", dim)) ||
-            (rc = check_f32(g, p + "ffn_norm.weight", dim)))
-            return rc;
-        for (const char* n : q4_names)
-            if ((rc = check_q4(g, p + n + ".weight"))) return rc;
+        for (const auto& t : tensors) {
+            const std::string name = p + t.name + ".weight";
+            if ((rc = t.norm ? check_f32(g, name, dim) : check_q4(g, name))) return rc;
+        }
     }
     return SLM_OK;
 }

@@ -86,9 +86,10 @@ class GgufWriter:
 
 
 def write_model(path, cfg: dict, w, tied: bool = False, arch: str = "llama",
-                rope_theta: float | None = None) -> None:
+                rope_theta: float | None = None, edit=None) -> None:
     """A whole model in the reference's tensor names (loader.rs:508-552) and
-    metadata keys (main.rs:36-46); w is an oracle ModelWeights."""
+    metadata keys (main.rs:36-46); w is an oracle ModelWeights.  edit, when
+    given, may change the writer (its tensor list) before the file is written."""
     g = GgufWriter()
     g.add_str("general.architecture", arch)
     g.add_u32(f"{arch}.block_count", cfg["num_layers"])
@@ -119,4 +120,6 @@ def write_model(path, cfg: dict, w, tied: bool = False, arch: str = "llama",
     g.add_tensor_f32("output_norm.weight", [len(w.output_norm)], w.output_norm)
     if not tied:
         g.add_tensor_q4_0("output.weight", [dim, vocab], w.lm_head)
+    if edit is not None:
+        edit(g)
     g.write(path)

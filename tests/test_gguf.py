@@ -237,3 +237,33 @@ def test_model_load_missing_tensor_and_wrong_type_before_upload(tmp_path):
         with pytest.raises(P.SlmAttnError) as ei:
             P.GgufModel(f, 1)
         assert ei.value.code == P.ERR_TYPE
+
+
+@pytest.mark.parametrize("first,code", [("attn_q", "ERR_NOT_FOUND"),
+                                        ("attn_norm", "ERR_TYPE")])
+def test_model_load_reports_the_first_fault_in_the_reference_order(tmp_path, first, code):
+    # Two faults in layer 1: attn_q missing and a norm of the wrong type.
+    # layer_weights resolves attn_norm, attn_q, attn_k, attn_v, attn_output,
+    # ffn_norm, gate, up, down in that order (loader.rs:508-520), so the error
+    # is the first fault met: with ffn_norm mistyped, TensorNotFound for
+    # attn_q; with attn_norm mistyped, TypeMismatch.
+    cfg, w, meta = _ref_model_meta()
+    bad_norm = "ffn_norm" if first == "attn_q" else "attn_norm"
+
+    def edit(g):
+        keep = []
+        for name, gtype, dims, raw in g.tensors:
+            if name == "blk.1.attn_q.weight":
+                continue
+            if name == f"blk.1.{bad_norm}.weight":
+                blocks = orc.quantize_q4_0(np.ones(cfg.dim, np.float32))
+                gtype, raw = GGML_Q4_0, blocks.tobytes()
+            keep.append((name, gtype, dims, raw))
+        g.tensors = keep
+
+    path = tmp_path / "two_faults.gguf"
+    write_model(path, meta, w, edit=edit)
+    with P.GgufFile(path) as f:
+        with pytest.raises(P.SlmAttnError) as ei:
+            P.GgufModel(f, meta["num_layers"])
+    assert ei.value.code == getattr(P, code), (ei.value.code, str(ei.value))
