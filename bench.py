@@ -168,17 +168,20 @@ def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768,
             ctx.decode_dev(l, pos, q[l].data_ptr(), k[l].data_ptr(), v[l].data_ptr(),
                            out[l].data_ptr())
 
-    for _ in range(warmup):
+    # The last (up to) two of the warm-up steps are queued after the
+    # synchronize, right ahead of the timed ones: after a synchronize the GPU
+    # idles and its clock takes a while to come back (timed steps that
+    # started from an idle GPU read ~3% slower over 20 steps), while steps
+    # that follow each other, as in serving, do not.  The number of untimed
+    # steps before the timed ones stays `warmup`.
+    queued = min(2, warmup)
+    for _ in range(warmup - queued):
         step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    # Two more untimed steps queued right before the timed ones: after the
-    # synchronize the GPU is idle and its clock takes a while to come back,
-    # which read ~3% slower over the 20 timed steps than steps that follow
-    # each other as in serving.
-    step()
-    step()
+    for _ in range(queued):
+        step()
     e0.record(stream)
     for _ in range(steps):
         step()
@@ -213,7 +216,10 @@ def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768,
         e1.record(stream)
         torch.cuda.synchronize()
         ms_s = e0.elapsed_time(e1)
-        steady = {"warmup_steps": warmup + steady_warmup, "steps": steps,
+        # untimed steps before this window: the warm-up, the timed steps, the
+        # profiled pass (one step and `steps` more) and steady_warmup
+        steady = {"warmup_steps": warmup + steps + 1 + steps + steady_warmup,
+                  "steady_warmup_steps": steady_warmup, "steps": steps,
                   "ms_per_step": round(ms_s / steps, 5),
                   "gbs": round(step_bytes * steps / (ms_s / 1e3) / 1e9, 2)}
     graph_us = None
@@ -255,6 +261,7 @@ def bench_decode_32k(torch, P, steps: int, warmup: int, ctx_len: int = 32768,
         "splits": ns, "tile": tile, "finite": finite,
         "combine_avg_us": comb_ms / max(n_comb, 1) * 1e3,
         "steady": steady, "graph_us_per_layer_step": graph_us,
+        "warmup_queued": queued,
         "_check": check,
     }
 
@@ -716,15 +723,54 @@ def bench_workloads(torch, P) -> tuple[list, list]:
         q, k, v = (torch.from_numpy(a).cuda() for a in (qh, kh, vh))
         o = torch.empty(layers, rows, dim, device="cuda")
 
+        def run_prefill(l):
+            ctx.prefill_dev(l, pre, npf, q[l].data_ptr(), k[l].data_ptr(), v[l].data_ptr(),
+                            o[l].data_ptr())
+
+        def run_decode(l):
+            for st in range(nd):
+                r = npf + st
+                ctx.decode_dev(l, pre + r, q[l, r].data_ptr(), k[l, r].data_ptr(),
+                               v[l, r].data_ptr(), o[l, r].data_ptr())
+
         def run():
             for l in range(layers):
                 if npf:
-                    ctx.prefill_dev(l, pre, npf, q[l].data_ptr(), k[l].data_ptr(),
-                                    v[l].data_ptr(), o[l].data_ptr())
-                for st in range(nd):
-                    r = npf + st
-                    ctx.decode_dev(l, pre + r, q[l, r].data_ptr(), k[l, r].data_ptr(),
-                                   v[l, r].data_ptr(), o[l, r].data_ptr())
+                    run_prefill(l)
+                run_decode(l)
+
+        def prefills():
+            for l in range(layers):
+                run_prefill(l)
+
+        def decodes():
+            for l in range(layers):
+                run_decode(l)
+
+        def graph_time(fn):
+            """fn's launches recorded once as a HIP graph, replayed with one
+            host call: their device time without the per-call host cost
+            (None, with the reason logged, if recording fails)."""
+            graph = None
+            try:
+                ctx.capture_begin()
+                try:
+                    fn()
+                finally:  # the stream leaves capture mode whatever happened
+                    graph = ctx.capture_end()
+                ctx.graph_launch(graph)
+                torch.cuda.synchronize()
+                e0.record(stream)
+                ctx.graph_launch(graph)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1)
+            except P.SlmAttnError as exc:
+                log(f"{name}: graph replay not measured: {exc}")
+                return None
+            finally:
+                if graph is not None:
+                    graph.close()
 
         run()
         torch.cuda.synchronize()
@@ -734,29 +780,12 @@ def bench_workloads(torch, P) -> tuple[list, list]:
         e1.record(stream)
         torch.cuda.synchronize()
         wall_ms = e0.elapsed_time(e1)
-        # the same pass recorded once as a HIP graph and replayed with one
-        # host call: the dispatch cost without the per-call host round trip
-        # (reported as null, with the reason logged, if recording fails)
-        graph_ms = None
-        graph = None
-        try:
-            ctx.capture_begin()
-            try:
-                run()
-            finally:  # the stream leaves capture mode whatever happened
-                graph = ctx.capture_end()
-            ctx.graph_launch(graph)
-            torch.cuda.synchronize()
-            e0.record(stream)
-            ctx.graph_launch(graph)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            graph_ms = e0.elapsed_time(e1)
-        except P.SlmAttnError as exc:
-            log(f"{name}: graph replay not measured: {exc}")
-        finally:
-            if graph is not None:
-                graph.close()
+        # the whole pass, then its prefill launches and its decode launches
+        # apart (the layers' caches are independent, so the two orders give
+        # the same work), each as a replayed graph
+        graph_ms = graph_time(run)
+        graph_pf_ms = graph_time(prefills) if npf else None
+        graph_dec_ms = graph_time(decodes)
         ctx.profile(True)
         run()
         prof = ctx.profile_read()
@@ -765,10 +794,19 @@ def bench_workloads(torch, P) -> tuple[list, list]:
         dec_bytes = layers * sum(4 * (2 * (p + 1) * kvd + 2 * dim + 4 * kvd)
                                  for p in range(pre + npf, pre + npf + nd))
         kern = {kind: round(ms, 4) for kind, (cnt, ms) in prof.items() if cnt}
-        pf_ms = prof["prefill"][1] + prof["append"][1]
-        dec_ms = prof["decode"][1] + prof["combine"][1]
+        # Rates from device time: the graph replays of the prefill launches
+        # and of the decode launches.  Sums of launch-stamped events overstate
+        # short kernels (an empty kernel stamps 3.9-4.0 us, and costs 2.4 us
+        # back to back), so they are the fallback only.
+        pf_ms = graph_pf_ms or (prof["prefill"][1] + prof["append"][1])
+        dec_ms = graph_dec_ms or (prof["decode"][1] + prof["combine"][1])
         rec = {"workload": name, "wall_ms": round(wall_ms, 4),
                "graph_ms": round(graph_ms, 4) if graph_ms else None,
+               "graph_prefill_ms": round(graph_pf_ms, 4) if graph_pf_ms else None,
+               "graph_decode_ms": round(graph_dec_ms, 4) if graph_dec_ms else None,
+               "rates_from": ("graph replays of the prefill and of the decode launches"
+                              if (graph_dec_ms and (graph_pf_ms or not npf))
+                              else "sums of launch-stamped kernel events"),
                "kernel_ms": round(sum(ms for _, ms in prof.values()), 4),
                "kernel_ms_by_kind": kern,
                "launches": int(sum(cnt for cnt, _ in prof.values())),
@@ -826,10 +864,10 @@ def cpu_configs(checks: list) -> list:
     """CPU baseline leg for the configurations: the oracle (the reference's
     single-threaded attention arithmetic restated in C, one host core) on the
     same inputs as the GPU run, timed, and used as the checker of the GPU
-    outputs and appended cache rows.  C1-C3 run in full; C4 times its prefill
-    on 24 rows spread over the 4096 and 4 of its 128 decode steps, C5 3 of its
-    64 decode steps (the other rows are appended to the oracle's cache
-    untimed), and the full-run CPU time is extrapolated by flops / bytes."""
+    outputs and appended cache rows.  C1-C4 run in full (C4: the 4096-row
+    prefill and all 128 decode steps, ~20 s); C5 times its first four decode
+    steps and its last (the others are appended to the oracle's cache
+    untimed), and its full-run CPU time is extrapolated by bytes."""
     sys.path.insert(0, str(REPO))
     from oracle import py_oracle as orc
 
@@ -844,7 +882,7 @@ def cpu_configs(checks: list) -> list:
         if pre:
             om.k_cache(0)[:pre] = ch["pre_k"]
             om.v_cache(0)[:pre] = ch["pre_v"]
-        full = pre == 0 and npf <= 1024  # C1-C3
+        full = pre == 0  # C1-C4
         err, t_oracle = None, 0.0
         est_ms, sample = None, "full run"
         if full:
@@ -874,7 +912,7 @@ def cpu_configs(checks: list) -> list:
                     f_smp += 4 * hd * h * (pre + b + 1)
                     err = _merge_errs(err, _errs(got[0, b], r))
                 f_all = 4 * hd * h * sum(range(pre + 1, pre + npf + 1))
-            steps = sorted({0, 1, nd // 2, nd - 1} if npf else {0, 1, nd - 1})
+            steps = sorted({0, 1, nd // 2, nd - 1} if npf else {0, 1, 2, 3, nd - 1})
             for st in range(nd):
                 p = pre + npf + st
                 bp = 4 * (2 * (p + 1) * kvd + 2 * dim + 4 * kvd)
@@ -1167,6 +1205,9 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        # of those untimed steps, how many were queued after the last
+        # synchronize, right ahead of the timed ones (the rest ran before it)
+        "warmup_queued": d["warmup_queued"],
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
