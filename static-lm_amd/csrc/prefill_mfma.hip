@@ -138,12 +138,24 @@ constexpr int prefill_waves_per_simd() {
 // DMA: K/V tiles go straight from memory to LDS (buffer loads with the lds
 // bit) into two buffers, with no registers held for the next tile; four waves
 // per SIMD.  Otherwise the next tile is prefetched into registers.
+//
+// KSP (register prefetch only): key splits.  The workgroup holds KSP sets of
+// HW*QS waves; set k attends tiles k, k + KSP, k + 2*KSP, ... of its query
+// block, the KSP tiles of a step loaded together into KSP LDS slots, and at
+// the end sets 1..KSP-1 hand their (max, sum, O) to set 0 through LDS, which
+// merges them in set order.  Used for short prefills with one head per
+// workgroup (head_dim <= 64): the heaviest causal block's key tiles are
+// walked by KSP SIMDs instead of one.  (Splitting keys among the waves of a workgroup that
+// already has a wave on every SIMD gains nothing: the per-SIMD MFMA work of
+// the heaviest block stays the same.)
 template <int HD, int HW, int QS, int NQT, int kKT = 32, int NB = 1, bool PRIO = false,
-          bool DMA = false>
-__global__ __launch_bounds__(64 * HW * QS, (DMA ? 4 : prefill_waves_per_simd<HD, HW>())) void
+          bool DMA = false, int KSP = 1>
+__global__ __launch_bounds__(64 * HW * QS * KSP,
+                             (DMA ? 4 : prefill_waves_per_simd<HD, HW>())) void
 prefill_mfma_kernel(PrefillParams p) {
     constexpr int KS = kKT / 16;  // 16-key sub-tiles per LDS tile
-    constexpr int NW = HW * QS;
+    constexpr int NWS = HW * QS;  // waves of one key split
+    constexpr int NW = NWS * KSP;
     constexpr int NT = 64 * NW;
     using Lds = std::conditional_t<DMA, PrefillLdsDma<HD>, PrefillLds<HD>>;
     constexpr int LDK = Lds::LDK;
@@ -153,7 +165,7 @@ prefill_mfma_kernel(PrefillParams p) {
     constexpr int QPW = 16 * NQT; // query rows per wave
     constexpr int QB = QPW * QS;  // query rows per workgroup
     constexpr int F4 = kKT * HD / 4;          // float4 per K (or V) tile
-    constexpr int NPF = (F4 + NT - 1) / NT;   // float4 per thread per tile
+    constexpr int NPF = (F4 * KSP + NT - 1) / NT;  // float4 per thread per step
     static_assert(DPL % 4 == 0 && HD % 16 == 0, "head_dim must be a multiple of 16");
     // PV operands.  With NDT a multiple of 4, row m of each 16-dim O^T tile
     // maps to lane m's own NDT contiguous head dims, read from the V tile as
@@ -164,10 +176,15 @@ prefill_mfma_kernel(PrefillParams p) {
     constexpr int VC = VEC_V ? NDT / 4 : 1;
 
     // NB LDS buffers: with two, a tile is stored while the other is read and
-    // one barrier per tile suffices
+    // one barrier per tile suffices.  With key splits, KSP tile slots (one
+    // buffer each), in one array so the merge at the end can reuse it whole.
     static_assert(!DMA || NB == 2, "DMA tiles use two buffers");
-    __shared__ __align__(16) float sKb[NB][kKT * LDK];
-    __shared__ __align__(16) float sVb[NB][kKT * LDV];
+    static_assert(KSP == 1 || (!DMA && NB == 1), "key splits: register prefetch, one buffer");
+    static_assert(KSP == 1 || F4 % 64 == 0, "key splits: a wave's tile loads in one slot");
+    constexpr int NSLOT = NB * KSP;
+    __shared__ __align__(16) float s_tiles[NSLOT * kKT * (LDK + LDV)];
+    float(*sKb)[kKT * LDK] = reinterpret_cast<float(*)[kKT * LDK]>(s_tiles);
+    float(*sVb)[kKT * LDV] = reinterpret_cast<float(*)[kKT * LDV]>(s_tiles + NSLOT * kKT * LDK);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -178,7 +195,8 @@ prefill_mfma_kernel(PrefillParams p) {
     const int lr = lane & 15;
     const int lg = lane >> 4;
     const int hw = wave % HW;
-    const int qs = wave / HW;
+    const int qs = (wave / HW) % QS;
+    const int kspl = wave / NWS;  // key split
 
     // blockIdx.x = query block * head groups + head group: consecutive
     // workgroups go round-robin to the 8 XCDs, so with 8 head groups each XCD's
@@ -294,7 +312,7 @@ prefill_mfma_kernel(PrefillParams p) {
     } else {
 #pragma unroll
         for (int i = 0; i < NPF; ++i) {
-            const int f = tid + i * NT;
+            const int f = (tid + i * NT) % F4;  // within its tile slot
             t_off[i] = ((f / (HD / 4)) * p.kv_dim + (f % (HD / 4)) * 4) * 4;
         }
     }
@@ -306,6 +324,45 @@ prefill_mfma_kernel(PrefillParams p) {
     };
     float4 pk[DMA ? 1 : NPF], pv[DMA ? 1 : NPF];
     static_assert(tile_range_fits(kKT, kMaxKvDim), "tile ranges must fit 32 bits");
+    // Register prefetch of the KSP tiles from tile kt0: this thread's float4 i
+    // belongs to slot (wave*64 + i*NT) / F4 (whole waves per slot, so the
+    // slot and its descriptor are wave-uniform); slots past the last tile
+    // load nothing.
+    auto prefetch_regs = [&](int kt0) __attribute__((always_inline)) {
+        if constexpr (KSP == 1) {
+            // one tile: one descriptor for all of this thread's loads
+            const int kb = kt0 * kKT;
+            const int bytes = (int)tile_range_bytes(kv_len, kb, kKT, p.kv_dim);
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(kg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(vg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
+#pragma unroll
+            for (int i = 0; i < NPF; ++i) {
+                if (tid + i * NT < F4) {
+                    pk[i] = bload(rk, t_off[i]);
+                    pv[i] = bload(rv, t_off[i]);
+                }
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < NPF; ++i) {
+            if (wave * 64 + i * NT >= F4 * KSP) continue;  // uniform
+            const int slot = (wave * 64 + i * NT) / F4;
+            const int kb = (kt0 + slot) * kKT;
+            if (kt0 + slot >= n_tiles) continue;  // uniform
+            const int bytes = (int)tile_range_bytes(kv_len, kb, kKT, p.kv_dim);
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(kg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(vg + (long)kb * p.kv_dim), 0, bytes, 0x00020000);
+            if (tid + i * NT < F4 * KSP) {
+                pk[i] = bload(rk, t_off[i]);
+                pv[i] = bload(rv, t_off[i]);
+            }
+        }
+    };
     auto prefetch = [&](int kb, int buf) __attribute__((always_inline)) {
         // rows kb .. min(kv_len, kb + kKT) - 1: bounded by the tile (one
         // layer's K slice may pass 4 GiB)
@@ -333,14 +390,9 @@ prefill_mfma_kernel(PrefillParams p) {
                              "s"(rv), "{m0}"(lv) : "memory");
             }
         } else {
-            (void)buf;
-#pragma unroll
-            for (int i = 0; i < NPF; ++i) {
-                if (tid + i * NT < F4) {
-                    pk[i] = bload(rk, t_off[i]);
-                    pv[i] = bload(rv, t_off[i]);
-                }
-            }
+            (void)buf;  // register prefetch goes through prefetch_regs
+            (void)rk;
+            (void)rv;
         }
     };
 
@@ -396,23 +448,32 @@ prefill_mfma_kernel(PrefillParams p) {
                 for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[ks][qt][r]);
             }
             mx = rows_max(mx);  // of s - om
-            // the first tile always holds key 0 <= qpos, so mx is finite there
+            // Without key splits the first tile always holds key 0 <= qpos, so
+            // mx is finite there.  With them, the first tile a split attends
+            // may mask every key of a query (positions below the tile): such a
+            // lane has seen no key yet and keeps its empty state (max -inf,
+            // no offset), or exp2(-inf - -inf) would make it NaN.
             if (__any(mx > lim[qt])) {  // wave-uniform
                 const float mn = fmaxf(m[qt], mx + om[qt]);
-                const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
+                bool none = false;
+                if constexpr (KSP > 1) none = mn == -INFINITY;
+                const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m[qt] - mn);
                 l[qt] *= alpha;
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
-                const float d = mn - om[qt];  // this tile's scores move to the new offset
+                // this tile's scores move to the new offset
+                const float d = none ? 0.0f : mn - om[qt];
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) s[ks][qt][r] -= d;
                 }
                 m[qt] = mn;
-                om[qt] = mn;
-                lim[qt] = kLazyRescale;
-                negm[qt] = floatx4{-mn, -mn, -mn, -mn};
+                if (!none) {
+                    om[qt] = mn;
+                    lim[qt] = kLazyRescale;
+                    negm[qt] = floatx4{-mn, -mn, -mn, -mn};
+                }
             }
             float ps = 0.0f;  // starts at the first term (0 + e is e exactly, e >= 0)
 #pragma unroll
@@ -471,7 +532,10 @@ prefill_mfma_kernel(PrefillParams p) {
         if (PRIO) __builtin_amdgcn_s_setprio(0);
     };
 
-    prefetch(0, 0);
+    if constexpr (DMA)
+        prefetch(0, 0);
+    else
+        prefetch_regs(0);
     if constexpr (DMA) {
         // Two tiles per trip, so each tile's buffer is a compile-time constant:
         // the LDS read addresses are then loop-invariant registers plus
@@ -492,24 +556,99 @@ prefill_mfma_kernel(PrefillParams p) {
             if (it + 1 < n_tiles) step(it + 1, std::integral_constant<int, 1>());
         }
     } else {
-        for (int it = 0; it < n_tiles; ++it) {
-            const int kb = it * kKT;
-            float* sK = sKb[it % NB];
-            float* sV = sVb[it % NB];
-            if (NB == 1) __syncthreads();  // every wave is done with the previous tile
+        // step st: tiles st*KSP .. st*KSP + KSP - 1 in slots 0..KSP-1; key
+        // split kspl attends slot kspl
+        const int n_steps = (n_tiles + KSP - 1) / KSP;
+        for (int st = 0; st < n_steps; ++st) {
+            const int kt0 = st * KSP;
+            if (NB == 1) __syncthreads();  // every wave is done with the previous tiles
 #pragma unroll
             for (int i = 0; i < NPF; ++i) {
                 const int f = tid + i * NT;
-                if (f < F4) {
-                    const int r = f / (HD / 4), ch = f % (HD / 4);
-                    *reinterpret_cast<float4*>(&sK[r * LDK + 4 * (ch ^ Lds::k_swz(r))]) = pk[i];
-                    *reinterpret_cast<float4*>(&sV[r * LDV + 4 * ch]) = pv[i];
+                if constexpr (KSP == 1) {
+                    if (f < F4) {
+                        const int r = f / (HD / 4), ch = f % (HD / 4);
+                        float* sK = sKb[st % NB];
+                        float* sV = sVb[st % NB];
+                        *reinterpret_cast<float4*>(&sK[r * LDK + 4 * (ch ^ Lds::k_swz(r))]) =
+                            pk[i];
+                        *reinterpret_cast<float4*>(&sV[r * LDV + 4 * ch]) = pv[i];
+                    }
+                } else {
+                    const int slot = (wave * 64 + i * NT) / F4;  // uniform
+                    if (f < F4 * KSP && kt0 + slot < n_tiles) {
+                        const int fr = f % F4;
+                        const int r = fr / (HD / 4), ch = fr % (HD / 4);
+                        float* sK = sKb[(st % NB) * KSP + slot];
+                        float* sV = sVb[(st % NB) * KSP + slot];
+                        *reinterpret_cast<float4*>(&sK[r * LDK + 4 * (ch ^ Lds::k_swz(r))]) =
+                            pk[i];
+                        *reinterpret_cast<float4*>(&sV[r * LDV + 4 * ch]) = pv[i];
+                    }
                 }
             }
             __syncthreads();
-            if (it + 1 < n_tiles) prefetch(kb + kKT, 0);
-            if (wave_rows == 0 || kb > wave_last_pos) continue;  // wave-uniform
-            attend(kb, sK, sV);
+            if (st + 1 < n_steps) prefetch_regs(kt0 + KSP);
+            const int it = kt0 + kspl;
+            const int kb = it * kKT;
+            if (it >= n_tiles || wave_rows == 0 || kb > wave_last_pos) continue;  // uniform
+            attend(kb, sKb[(st % NB) * KSP + kspl], sVb[(st % NB) * KSP + kspl]);
+        }
+    }
+
+    if constexpr (KSP > 1) {
+        // Merge of the key splits: sets 1..KSP-1 write each lane's O
+        // registers, max and sum partial to the tile LDS (lane-contiguous,
+        // no bank conflicts), set 0 folds them in set order: M = max of the
+        // maxima, every state scaled by 2^(m - M) (0 for a set that saw no
+        // key), then summed.
+        constexpr int NR = NQT * (NDT * 4 + 2);  // floats per lane
+        static_assert((KSP - 1) * NWS * 64 * NR <= NSLOT * kKT * (LDK + LDV),
+                      "the merge fits the tile LDS");
+        __syncthreads();  // every wave is done with the tiles
+        const int ws = wave % NWS;
+        if (kspl > 0) {
+            float* dst = s_tiles + ((kspl - 1) * NWS + ws) * NR * 64 + lane;
+            int r = 0;
+#pragma unroll
+            for (int qt = 0; qt < NQT; ++qt) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dst[64 * r++] = o[qt][dt][e];
+                dst[64 * r++] = m[qt];
+                dst[64 * r++] = l[qt];
+            }
+        }
+        __syncthreads();
+        if (kspl > 0) return;  // no barrier follows
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+            constexpr int MOFF = NDT * 4;  // m, then l, after a query tile's O
+            float mk[KSP];
+            mk[0] = m[qt];
+            float mx = m[qt];
+#pragma unroll
+            for (int k = 1; k < KSP; ++k) {
+                mk[k] = s_tiles[((k - 1) * NWS + ws) * NR * 64 + lane +
+                                64 * (qt * (MOFF + 2) + MOFF)];
+                mx = fmaxf(mx, mk[k]);
+            }
+            const float s0 = __builtin_amdgcn_exp2f(m[qt] - mx);
+            l[qt] *= s0;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= s0;
+#pragma unroll
+            for (int k = 1; k < KSP; ++k) {
+                const float* src = s_tiles + ((k - 1) * NWS + ws) * NR * 64 + lane +
+                                   64 * qt * (MOFF + 2);
+                const float sk = __builtin_amdgcn_exp2f(mk[k] - mx);
+                l[qt] += src[64 * (MOFF + 1)] * sk;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[qt][dt][e] += src[64 * (dt * 4 + e)] * sk;
+            }
         }
     }
 
@@ -566,7 +705,7 @@ Tiling pick_tiling(int kv_mul) {
     return {1, 4};
 }
 
-template <int HD, int HW, int QS>
+template <int HD, int HW, int QS, int KSP>
 hipError_t launch_t(const Shape& s, const PrefillParams& pp, hipStream_t st) {
     // 16 query rows per wave: measured on MI355X (hd 128, 4096 rows) 57% of
     // the fp32 MFMA peak against 47% with 32 rows per wave, because the lower
@@ -575,8 +714,8 @@ hipError_t launch_t(const Shape& s, const PrefillParams& pp, hipStream_t st) {
     constexpr int QB = 16 * NQT * QS;
     const int n_qb = (pp.n + QB - 1) / QB;
     const dim3 grid(n_qb * (s.num_heads / HW));
-    hipLaunchKernelGGL((prefill_mfma_kernel<HD, HW, QS, NQT>), grid, dim3(64 * HW * QS), 0,
-                       st, pp);
+    hipLaunchKernelGGL((prefill_mfma_kernel<HD, HW, QS, NQT, 32, 1, false, false, KSP>), grid,
+                       dim3(64 * HW * QS * KSP), 0, st, pp);
     return hipGetLastError();
 }
 
@@ -600,10 +739,24 @@ hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
             return hipGetLastError();
         }
     }
-    if (t.hw == 4) return launch_t<HD, 4, 1>(s, pp, st);
-    if (t.hw == 3) return launch_t<HD, 3, 1>(s, pp, st);
-    if (t.hw == 2) return launch_t<HD, 2, 2>(s, pp, st);
-    return launch_t<HD, 1, 4>(s, pp, st);
+    // Short prefills, head_dim <= 64: when the head-group tiling gives fewer
+    // than two workgroups per CU, one head and one 16-row query block per
+    // workgroup with its key tiles split over four waves, as long as the
+    // heaviest block keeps two tiles per split: more workgroups, and the
+    // heaviest block's tiles walked by four SIMDs instead of one.  (Each
+    // thread then prefetches four tiles' share: 169 VGPRs at hd 64, 312 at
+    // hd 128.)  A pure function of the batch, the shape and the CU count.
+    if constexpr (HD <= 64) {
+        constexpr int KSP = 4;
+        const int qs = t.hw == 1 ? 4 : t.hw == 2 ? 2 : 1;
+        const long wgs = (long)((pp.n + 16 * qs - 1) / (16 * qs)) * (s.num_heads / t.hw);
+        const long tiles = ((long)pp.start + pp.n + 31) / 32;  // the heaviest block's
+        if (wgs < 2L * s.cus && tiles >= 2L * KSP) return launch_t<HD, 1, 1, KSP>(s, pp, st);
+    }
+    if (t.hw == 4) return launch_t<HD, 4, 1, 1>(s, pp, st);
+    if (t.hw == 3) return launch_t<HD, 3, 1, 1>(s, pp, st);
+    if (t.hw == 2) return launch_t<HD, 2, 2, 1>(s, pp, st);
+    return launch_t<HD, 1, 4, 1>(s, pp, st);
 }
 
 }  // namespace
