@@ -337,6 +337,60 @@ def bench_prefill_4k(torch, P, reps: int) -> dict:
             "profile": prof}
 
 
+# Short causal prefills (start 0): name, dim, heads, KV heads, theta, rows.  The
+# model prompt's length on the Llama-3-8B shape and the configurations' own
+# short prefills on the SmolLM2-135M and Stories-15M shapes.
+PREFILL_SHORT = [("llama3-8b", 4096, 32, 8, 5e5, 512), ("llama3-8b", 4096, 32, 8, 5e5, 1024),
+                 ("llama3-8b", 4096, 32, 8, 5e5, 2048), ("smollm2-135m", 576, 9, 3, 1e5, 512),
+                 ("stories15m", 288, 6, 6, 1e4, 256)]
+
+
+def bench_prefill_short(torch, P, reps: int = 20) -> list:
+    """Each short prefill of PREFILL_SHORT called back to back: per-call time
+    (append + prefill kernels) and the prefill kernel's launch-stamped time,
+    with its algorithmic TFLOP/s and fraction of the fp32 MFMA peak."""
+    stream = torch.cuda.current_stream()
+    out = []
+    for name, dim, h, kvh, theta, n in PREFILL_SHORT:
+        hd = dim // h
+        kvd = hd * kvh
+        ctx = P.AttentionContext(dim, h, kvh, n, 1, theta)
+        ctx.set_stream(stream.cuda_stream)
+        q = torch.randn(n, dim, device="cuda") * 0.5
+        k = torch.randn(n, kvd, device="cuda") * 0.5
+        v = torch.randn(n, kvd, device="cuda") * 0.5
+        o = torch.empty(n, dim, device="cuda")
+
+        def run():
+            ctx.prefill_dev(0, 0, n, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr())
+
+        for _ in range(5):
+            run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        call_us = e0.elapsed_time(e1) / reps * 1e3
+        ctx.profile(True)
+        for _ in range(reps):
+            run()
+        cnt, kms = ctx.profile_read()["prefill"]
+        ctx.profile(False)
+        ctx.close()
+        kus = kms / max(cnt, 1) * 1e3
+        flops = 4 * hd * h * (n * (n + 1) // 2)  # causal pairs, start 0
+        out.append({"workload": f"{name} {h}/{kvh} heads hd{hd}, {n} rows", "rows": n,
+                    "call_us": round(call_us, 2), "kernel_us_stamped": round(kus, 2),
+                    "kernel_tflops": round(flops / (kus / 1e6) / 1e12, 2),
+                    "kernel_frac_fp32_mfma": round(flops / (kus / 1e6) / 1e12
+                                                   / FP32_MFMA_PEAK_TFLOPS, 4)})
+        log(f"prefill {name} {n} rows: {call_us:.1f} us per call, kernel {kus:.1f} us "
+            f"({out[-1]['kernel_tflops']:.1f} TFLOP/s)")
+    return out
+
+
 def random_q4_blocks(rng, rows: int, cols: int) -> np.ndarray:
     """Random BlockQ4_0 bytes (random nibbles, f16 scales in [1e-3, 1e-2]):
     projection timing does not depend on the values."""
@@ -1022,6 +1076,9 @@ def main() -> int:
     ap.add_argument("--model-only", action="store_true",
                     help="only the whole model (prefill and greedy decode, Llama-3-8B shape); "
                          "prints its own JSON line, not the headline one")
+    ap.add_argument("--prefill-short-only", action="store_true",
+                    help="only the short prefills (512-2048 rows, Llama-3-8B, SmolLM2-135M "
+                         "and Stories-15M shapes)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode measurements (8 layers at 32767, 131072..131135, 8 layers "
                          "at 4095 and at 599; a short program for kernel traces); prints its own "
@@ -1093,6 +1150,10 @@ def main() -> int:
                           "kernel_avg_ms": pf["kernel_avg_ms"]}))
         return 0
 
+    if args.prefill_short_only:
+        print(json.dumps({"prefill_short": bench_prefill_short(torch, P)}))
+        return 0
+
     if args.decode_only:
         d = bench_decode_32k(torch, P, args.steps, args.warmup)
         dl = bench_decode_131k(torch, P)
@@ -1114,6 +1175,8 @@ def main() -> int:
         log("prefill 4096")
         pf = bench_prefill_4k(torch, P, reps=max(10, args.steps // 5))
         log(f"prefill 4096: {pf['ms']:.3f} ms, {pf['tflops']:.2f} TFLOP/s")
+        log("short prefills")
+        pshort = bench_prefill_short(torch, P)
         log("decode @131k")
         dl = bench_decode_131k(torch, P)
         log("decode at short contexts")
@@ -1168,6 +1231,7 @@ def main() -> int:
                 "kernel_avg_ms": pf["kernel_avg_ms"], "kernel_tflops": pf["kernel_tflops"],
                 "workload": "causal prefill 4096 tokens, 1 layer, start 0",
             },
+            "prefill_short": pshort,
             "decode_short": {
                 "workload": "decode at position ctx-1 through 8 layers of the Llama-3-8B head "
                             "shape, steps back to back (decode + split merge per layer)",
