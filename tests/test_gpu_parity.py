@@ -487,6 +487,50 @@ def test_prefill_shapes_and_ragged_batches(dim, heads, kv_heads, start, n):
                              what=f"row {b} at {start + b}")
 
 
+def takes_key_splits(dim, heads, kv_heads, start, n, cus=256):
+    """Whether a prefill takes the one-head key-split kernel (prefill_mfma.hip,
+    launch_hd): head_dim <= 64, fewer than two workgroups per CU in the
+    head-group tiling, at least 8 key tiles in the heaviest block."""
+    hd = dim // heads
+    kv_mul = heads // kv_heads
+    hw = 4 if kv_mul % 4 == 0 else 3 if kv_mul % 3 == 0 else 2 if kv_mul % 2 == 0 else 1
+    qs = {4: 1, 3: 1, 2: 2, 1: 4}[hw]
+    wgs = -(-n // (16 * qs)) * (heads // hw)
+    return hd <= 64 and wgs < 2 * cus and (start + n + 31) // 32 >= 8
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads", [
+    (576, 9, 3),     # hd 64, kv_mul 3 (SmolLM2-135M)
+    (1024, 16, 16),  # hd 64, MHA
+    (288, 6, 6),     # hd 48 (Stories-15M)
+    (512, 16, 4),    # hd 32, kv_mul 4
+    (256, 16, 8),    # hd 16, kv_mul 2
+])
+@pytest.mark.parametrize("start,n", [(0, 300), (37, 290), (200, 77), (250, 1)])
+def test_prefill_key_splits_every_row(dim, heads, kv_heads, start, n):
+    # The short-prefill kernel that splits a query block's key tiles over
+    # four waves (one head per workgroup): ragged row counts, a start past
+    # the first tiles (so a split's first tile can mask every key of some
+    # query), a single row; every row against the oracle, K/V rows bit for bit.
+    assert takes_key_splits(dim, heads, kv_heads, start, n)
+    rows = start + n
+    cfg = orc.Cfg(dim, heads, kv_heads, rows, 1, 1e4)
+    log(f"key-split prefill dim {dim} heads {heads}/{kv_heads} start {start} n {n}")
+    q = gen([81, dim, n], (rows, dim))
+    k = gen([82, dim, n], (rows, cfg.kv_dim))
+    v = gen([83, dim, n], (rows, cfg.kv_dim))
+    om = orc.OracleModel(cfg)
+    with P.AttentionContext(dim, heads, kv_heads, rows, 1) as ctx:
+        if start:
+            ctx.prefill(0, 0, q[:start], k[:start], v[:start])
+            om.prefill(0, 0, q[:start], k[:start], v[:start])
+        g = ctx.prefill(0, start, q[start:], k[start:], v[start:])
+        r = om.prefill(0, start, q[start:], k[start:], v[start:])
+        assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
+        assert_close(g, r, what=f"key-split prefill rows {start}..{rows - 1}")
+
+
 DECODE_SHAPES = [
     (64, 4, 4),      # hd 16
     (256, 8, 2),     # hd 32, kv_mul 4
