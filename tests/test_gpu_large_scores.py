@@ -55,6 +55,12 @@ SHAPES = {
     "hd48-gqa4": (1536, 32, 8, 1e4),   # hd 48: 4 lanes per position, LDS slot merge
     "stories15m": (288, 6, 6, 1e4),    # hd 48 without GQA (one head per workgroup)
     "smollm2": (576, 9, 3, 5e5),       # hd 64, GQA 3 (prefill: three heads per workgroup)
+    "hd96-gqa4": (3072, 32, 8, 1e4),   # hd 96: 8 lanes, four heads, third merge round
+    "hd96-mha": (768, 8, 8, 1e4),      # hd 96, one head per workgroup: LDS slot merge
+    "hd256-gqa4": (4096, 16, 4, 1e4),  # hd 256: 32 lanes per position, LDS slot merge
+    "hd32-gqa4": (1024, 32, 8, 1e4),   # hd 32: 4 lanes per position
+    "hd16-gqa4": (512, 32, 8, 1e4),    # hd 16: 2 lanes per position
+    "hd128-mha": (4096, 32, 32, 5e5),  # hd 128 without GQA: one head per workgroup
 }
 # per-head sharpness: q_h = F[h % 4] * base_g (+ a little noise)
 F = (1.0, 1.5, 0.8, 1.25)
@@ -164,7 +170,9 @@ def check_close_form(got, want, bar, what):
 # ---- decode ------------------------------------------------------------------
 
 DECODE_CASES = [("llama3-8b", 32767), ("llama3-8b", 131072), ("hd64-gqa4", 32767),
-                ("hd48-gqa4", 32767), ("stories15m", 49151)]
+                ("hd48-gqa4", 32767), ("stories15m", 49151), ("hd96-gqa4", 32767),
+                ("hd96-mha", 32767), ("hd256-gqa4", 32767), ("hd32-gqa4", 32767),
+                ("hd16-gqa4", 65535), ("hd128-mha", 32767)]
 KINDS = ("needle", "ramp", "far", "early", "appended")
 
 
@@ -301,10 +309,14 @@ def test_decode_large_scores_closed_form(name, p):
 # ---- prefill -----------------------------------------------------------------
 
 # (shape, start, n): the 4096-row Llama-3-8B-shape prefill takes the DMA-fed
-# kernel on 256 CUs; the others the register-prefetch kernel (hd 128 four
-# heads per workgroup, hd 64 three, hd 48 one head and four query blocks)
+# kernel on 256 CUs; the others the register-prefetch kernel: four heads per
+# workgroup at hd 128, 256 and 32, one head and four query blocks for the hd
+# 128 and hd 96 MHA shapes; the hd 64 (three heads), hd 48 and hd 16 shapes
+# give under two workgroups per CU at these lengths and take the one-head
+# kernel with the key tiles split over four waves
 PREFILL_CASES = [("llama3-8b", 0, 4096), ("llama3-8b", 24, 1000), ("smollm2", 0, 2048),
-                 ("stories15m", 0, 512)]
+                 ("stories15m", 0, 512), ("hd128-mha", 0, 2048), ("hd256-gqa4", 24, 1000),
+                 ("hd96-mha", 0, 1024), ("hd32-gqa4", 0, 1024), ("hd16-gqa4", 0, 512)]
 A = (4.0, 4.5, 5.0, 3.5)  # per-head size of q's large component
 
 
