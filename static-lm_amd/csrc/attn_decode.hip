@@ -22,8 +22,8 @@
 // bytes per group); each lane group keeps its own online-softmax state
 // (log2 domain) over the positions it sees.  States merge across lane groups
 // with shuffles and across waves through LDS; a sequence that fits one split
-// is written out directly, otherwise decode_combine_kernel merges the split
-// partials.  (Merging in the last workgroup to finish needs device-scope
+// is written out directly, otherwise decode_combine_kernel (up to 32 splits)
+// or decode_combine_wide_kernel merges the split partials.  (Merging in the last workgroup to finish needs device-scope
 // fences, which on this part write back and invalidate the whole L2: a
 // second small kernel is cheaper.)
 //
@@ -466,8 +466,9 @@ template <int HD>
 constexpr int combine_threads() {
     return (HD + 63) / 64 * 64;
 }
-// Split partials a merge thread loads per round (all of them for up to 32
-// splits, which covers the split policy on 256 CUs).
+// Split partials a merge thread loads per round: all of them for up to 32
+// splits (the Llama-3-8B shape's policy on 256 CUs); more splits go to
+// decode_combine_wide_kernel.
 constexpr int kCombineRound = 32;
 
 // Log-sum-exp merge of the split partials: one workgroup per head, one
@@ -535,6 +536,84 @@ __global__ __launch_bounds__(combine_threads<HD>()) void decode_combine_kernel(D
     if (has_d) p.out[h * HD + d] = acc / s_ltot;
 }
 
+// Threads of a wide merge workgroup, and the most splits it takes.
+constexpr int kCombineWideThreads = 1024;
+template <int HD>
+constexpr int combine_wide_max_splits() {
+    return kCombineWideThreads / combine_threads<HD>() * kCombineRound;
+}
+
+// The merge for more than kCombineRound splits (shapes with few KV-head
+// groups take up to 512/groups splits to fill the CUs: 170 for 3 groups).
+// decode_combine_kernel would take one dependent round of loads per 32
+// splits, and its wave 0 one more per 64 splits for the (max, sum) pairs
+// (ten memory round trips at 170 splits); here R = ceil(ns/32) rows of
+// threads, one thread per head dim in each, so every load is in flight at
+// once.  Thread t loads the pair of split t and thread (d, r) the partials
+// of dim d for splits 32r..32r+31.  The maxima reduce per wave and then over
+// the waves in wave order; each row sums its 32 splits in split order and the
+// rows are added in row order: a fixed function of n_splits, so results
+// reproduce bit for bit.  One memory round trip and three barriers.
+template <int HD>
+__global__ __launch_bounds__(kCombineWideThreads) void decode_combine_wide_kernel(
+    DecodeParams p) {
+    constexpr int HDT = combine_threads<HD>();
+    constexpr int kMaxRows = kCombineWideThreads / HDT;
+    __shared__ float s_w[kMaxRows * kCombineRound];
+    __shared__ float s_acc[kCombineWideThreads];
+    __shared__ float s_wmax[kCombineWideThreads / 64], s_wsum[kCombineWideThreads / 64];
+    const int h = blockIdx.x;
+    const int t = threadIdx.x;
+    const int d = t % HDT;
+    const int r = t / HDT;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int n_waves = blockDim.x >> 6;
+    const int rows = blockDim.x / HDT;
+    const int ns = p.n_splits;
+    const int u0 = r * kCombineRound;
+    const bool has_d = d < HD;
+    const float* src = p.part_o + (long)h * HD + (has_d ? d : 0);
+    const long stride = (long)p.num_heads * HD;
+
+    // the pair first, then the partials (indices clamped, every load
+    // unconditional: the compiler waits for the pair alone)
+    const float2* ml = reinterpret_cast<const float2*>(p.part_ml);
+    const float2 mlt = ml[(long)min(t, ns - 1) * p.num_heads + h];
+    asm volatile("" ::: "memory");
+    float x[kCombineRound];
+#pragma unroll
+    for (int u = 0; u < kCombineRound; ++u) x[u] = src[(long)min(u0 + u, ns - 1) * stride];
+
+    const float wm = wave_max(t < ns ? mlt.x : -INFINITY);
+    if (lane == 0) s_wmax[wave] = wm;
+    __syncthreads();
+    float mx = s_wmax[0];
+    for (int w = 1; w < n_waves; ++w) mx = fmaxf(mx, s_wmax[w]);
+    float wl = 0.0f;
+    if (t < ns) {
+        const float w = fast_exp2(mlt.x - mx);
+        s_w[t] = w;
+        wl = w * mlt.y;
+    }
+    wl = wave_sum(wl);
+    if (lane == 0) s_wsum[wave] = wl;
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kCombineRound; ++u)
+        if (u0 + u < ns) acc += s_w[u0 + u] * x[u];
+    s_acc[t] = acc;
+    __syncthreads();
+    if (r == 0 && has_d) {
+        float ltot = s_wsum[0];
+        for (int w = 1; w < n_waves; ++w) ltot += s_wsum[w];
+        float o = s_acc[d];
+        for (int rr = 1; rr < rows; ++rr) o += s_acc[rr * HDT + d];
+        p.out[h * HD + d] = o / ltot;
+    }
+}
+
 template <int HD, int GB>
 hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st, hipEvent_t ev0,
                     hipEvent_t ev1) {
@@ -551,6 +630,17 @@ hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st, hipE
 template <int HD>
 hipError_t launch_combine_t(const Shape& s, const DecodeParams& dp, hipStream_t st,
                             hipEvent_t ev0, hipEvent_t ev1) {
+    if (dp.n_splits > kCombineRound && dp.n_splits <= combine_wide_max_splits<HD>()) {
+        const int rows = (dp.n_splits + kCombineRound - 1) / kCombineRound;
+        const dim3 block(rows * combine_threads<HD>());
+        if (ev0 != nullptr && ev1 != nullptr)
+            hipExtLaunchKernelGGL(decode_combine_wide_kernel<HD>, dim3(s.num_heads), block, 0,
+                                  st, ev0, ev1, 0, dp);
+        else
+            hipLaunchKernelGGL(decode_combine_wide_kernel<HD>, dim3(s.num_heads), block, 0, st,
+                               dp);
+        return hipGetLastError();
+    }
     if (ev0 != nullptr && ev1 != nullptr)
         hipExtLaunchKernelGGL(decode_combine_kernel<HD>, dim3(s.num_heads),
                               dim3(combine_threads<HD>()), 0, st, ev0, ev1, 0, dp);

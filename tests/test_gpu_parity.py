@@ -598,6 +598,57 @@ def test_decode_split_tiles_across_shapes(dim, heads, kv_heads):
             assert_bitwise(ctx.kv_read(0, 1, p, 1), om.v_cache(0)[p:p + 1], f"V row {p}")
 
 
+# (dim, heads, kv_heads), split counts: shapes with few KV-head groups take up
+# to 512/groups splits (256/groups at hd 256); above 32 splits the merge runs
+# as one workgroup per head of ceil(n/32) rows of threads, up to 1024 threads
+# (512 splits at hd <= 64, 256 at hd 96/128, 128 at hd 256), beyond that
+# 32 splits per round
+MANY_SPLITS = [
+    ((128, 4, 1), (33, 512)),        # hd 32, one KV head: 2 and 16 rows of threads
+    ((128, 8, 2), (256,)),           # hd 16
+    ((256, 8, 2), (200,)),           # hd 32
+    ((288, 6, 6), (85,)),            # hd 48 MHA: the policy's cap
+    ((576, 9, 3), (48, 65, 170)),    # hd 64 GQA 3 (SmolLM2): 170 is its cap
+    ((2048, 32, 8), (64,)),          # hd 64 GQA 4
+    ((768, 8, 8), (64,)),            # hd 96: 128 threads per row
+    ((1024, 8, 2), (128,)),          # hd 128 GQA 4
+    ((1024, 4, 1), (128, 129, 256)), # hd 256: the wide merge's limit, then rounds
+]
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads,target",
+                         [s + (t,) for s, ts in MANY_SPLITS for t in ts])
+def test_decode_many_splits_against_oracle(dim, heads, kv_heads, target):
+    """Decode with append at a ragged length that gives `target` splits:
+    output against the oracle, the appended K/V row bit for bit, and a
+    second call giving the same bits."""
+    with P.AttentionContext(dim, heads, kv_heads, 16, 1) as probe:
+        cap, tile = probe.decode_splits(1 << 24)
+    assert target <= cap, (target, cap)
+    p = target * tile - tile // 3 - 1  # the last tile holds 2/3 of its rows
+    msl = p + 1
+    cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, 1e4)
+    kvd = cfg.kv_dim
+    om = orc.OracleModel(cfg)
+    with P.AttentionContext(dim, heads, kv_heads, msl, 1) as ctx:
+        ns, t = ctx.decode_splits(p + 1)
+        log(f"dim {dim} heads {heads}/{kv_heads}: decode at {p}, {ns} splits of {t}-row tiles")
+        assert (ns, t) == (target, tile)
+        kr = gen([91, dim, target], (p, kvd))
+        vr = gen([92, dim, target], (p, kvd))
+        ctx.kv_write(0, 0, 0, kr)
+        ctx.kv_write(0, 1, 0, vr)
+        om.k_cache(0)[:p] = kr
+        om.v_cache(0)[:p] = vr
+        q1, k1, v1 = gen([93, p], dim), gen([94, p], kvd), gen([95, p], kvd)
+        g = ctx.decode(0, p, q1, k1, v1)
+        r = om.decode(0, p, q1, k1, v1)
+        assert_close(g, r, what=f"decode at {p} ({ns} splits)")
+        assert_bitwise(ctx.kv_read(0, 0, p, 1), om.k_cache(0)[p:p + 1], f"K row {p}")
+        assert_bitwise(ctx.kv_read(0, 1, p, 1), om.v_cache(0)[p:p + 1], f"V row {p}")
+        assert_bitwise(ctx.decode(0, p, q1, k1, v1), g, f"second decode at {p}")
+
+
 def test_calibration_helpers_report_plausible_rates():
     r = P.calibrate_mfma_f32(iters=4000)
     log(f"fp32 MFMA {r['tflops']:.1f} TFLOP/s")
