@@ -23,9 +23,9 @@
 // (log2 domain) over the positions it sees.  States merge across lane groups
 // with shuffles and across waves through LDS; a sequence that fits one split
 // is written out directly, otherwise decode_combine_kernel (up to 32 splits)
-// or decode_combine_wide_kernel merges the split partials.  (Merging in the last workgroup to finish needs device-scope
-// fences, which on this part write back and invalidate the whole L2: a
-// second small kernel is cheaper.)
+// or decode_combine_wide_kernel merges the split partials.  (Merging in the
+// last workgroup to finish needs device-scope fences, which on this part
+// write back and invalidate the whole L2: a second small kernel is cheaper.)
 //
 // The workgroup owning position p does not read row p back: after its loop,
 // its wave 0 rotates k in registers with the reference's f32 arithmetic (no
@@ -53,15 +53,23 @@ constexpr int kMaxSplits = 1024;
 // HBM bandwidth; what matters beyond that is two waves per SIMD, which
 // 4-wave x 512 and 8-wave x 256 workgroups reach equally (interleaved
 // medians 46 us at 32k, 153 us at 131k); 8 waves halve the splits to merge.
+// MT: the most tiles a sequence may have and still run as one split (no
+// merge launch).  One split walks its tiles one memory round trip after
+// another, the split path costs a second launch.  Per layer-step (8 layers,
+// replayed as a graph, the two interleaved in one process), one split against
+// one tile per split: hd 128 at 4 tiles 6.89 against 6.93 us, at 5 tiles 7.80
+// against 6.95; hd 64 (GQA 3) at 5 tiles 6.81 against 5.99; hd 48 (6 heads)
+// at 3 tiles 7.52 against 7.01; hd 16, 32 and 96 at 4 tiles 9.70 / 9.78 /
+// 6.83 against 8.08 / 7.61 / 6.35; hd 256 at 5 tiles 5.91 against 5.84.
 template <int HD>
 struct DecodeCfg;
-template <> struct DecodeCfg<16> { static constexpr int LPG = 2, TP = 2, NW = 4; };
-template <> struct DecodeCfg<32> { static constexpr int LPG = 4, TP = 2, NW = 4; };
-template <> struct DecodeCfg<48> { static constexpr int LPG = 4, TP = 2, NW = 4; };
-template <> struct DecodeCfg<64> { static constexpr int LPG = 8, TP = 2, NW = 4; };
-template <> struct DecodeCfg<96> { static constexpr int LPG = 8, TP = 2, NW = 4; };
-template <> struct DecodeCfg<128> { static constexpr int LPG = 16, TP = 1, NW = 8; };
-template <> struct DecodeCfg<256> { static constexpr int LPG = 32, TP = 1, NW = 8; };
+template <> struct DecodeCfg<16> { static constexpr int LPG = 2, TP = 2, NW = 4, MT = 3; };
+template <> struct DecodeCfg<32> { static constexpr int LPG = 4, TP = 2, NW = 4, MT = 3; };
+template <> struct DecodeCfg<48> { static constexpr int LPG = 4, TP = 2, NW = 4, MT = 2; };
+template <> struct DecodeCfg<64> { static constexpr int LPG = 8, TP = 2, NW = 4, MT = 4; };
+template <> struct DecodeCfg<96> { static constexpr int LPG = 8, TP = 2, NW = 4, MT = 3; };
+template <> struct DecodeCfg<128> { static constexpr int LPG = 16, TP = 1, NW = 8, MT = 4; };
+template <> struct DecodeCfg<256> { static constexpr int LPG = 32, TP = 1, NW = 8, MT = 4; };
 
 template <int HD>
 constexpr int dec_span() {
@@ -70,8 +78,6 @@ constexpr int dec_span() {
 
 // Waves per CU one decode launch aims for on long sequences: two per SIMD.
 constexpr int kWavesPerCu = 8;
-// Sequences of at most this many tiles run as one split (no merge launch).
-constexpr int kMinTilesToSplit = 8;
 
 struct DecodeParams {
     const float* q;      // [dim]; rotated at p here when cos_t != nullptr
@@ -255,6 +261,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     if (wave >= NW / 2) __builtin_amdgcn_s_setprio(1);
     for (int tb = t0 + t_step; tb < t_end; tb += t_step) {
         load_tile(tb);
+        // With three float4 per lane and row (hd 48 and 96) the scheduler
+        // hoisted the first dot product right behind the first load, whose
+        // wait then split each tile into two memory round trips; the barrier
+        // sends every load of the tile first (unsplit decode 14.9 -> 13.3 us
+        // at 767 rows of the Stories-15M shape, 6.1 -> 5.6 us at 300 rows of
+        // hd 96).  The other layouts issue their loads first anyway, and
+        // there the barrier only reshuffled the code (2-3% slower at hd 16
+        // and 32, no change at hd 128).
+        if constexpr (NV == 3) __builtin_amdgcn_sched_barrier(0);
         attend_tile<LPG, NV, GB, TP>(qr, kr, vr, valid, m, l, o);
     }
     if (app_wave) {
@@ -674,6 +689,19 @@ int decode_waves(const Shape& s) {
     }
 }
 
+int decode_one_split_tiles(const Shape& s) {
+    switch (s.head_dim) {
+        case 16: return DecodeCfg<16>::MT;
+        case 32: return DecodeCfg<32>::MT;
+        case 48: return DecodeCfg<48>::MT;
+        case 64: return DecodeCfg<64>::MT;
+        case 96: return DecodeCfg<96>::MT;
+        case 128: return DecodeCfg<128>::MT;
+        case 256: return DecodeCfg<256>::MT;
+        default: return 1;
+    }
+}
+
 int decode_span(const Shape& s) {
     switch (s.head_dim) {
         case 16: return dec_span<16>();
@@ -701,16 +729,16 @@ void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* tile) 
     // one memory round trip, so one tile per split wins (Llama-3-8B shape at
     // 4096 rows: 15.0 us with 32 splits against 17.4 us with 16; SmolLM2 at
     // 768 rows: 10.8 us with 12 splits against 13.0 us with one).  Up to
-    // kMinTilesToSplit tiles the merge launch costs more than it saves, and
-    // a single split writes the output directly.  A pure function of
-    // seq_len, the shape and the CU count, so results reproduce run to run
-    // on a device.
+    // DecodeCfg::MT tiles (2-4 by head_dim) the merge launch costs more than
+    // it saves, and a single split writes the output directly.  A pure
+    // function of seq_len, the shape and the CU count, so results reproduce
+    // run to run on a device.
     const int it = decode_span(s);
     const int groups = decode_groups(s);
     const int wgs = kWavesPerCu * s.cus / decode_waves(s);
     const int want = groups >= wgs ? 1 : wgs / groups;
     const int tiles = (seq_len + it - 1) / it;
-    int ns = tiles <= kMinTilesToSplit ? 1 : (tiles < want ? tiles : want);
+    int ns = tiles <= decode_one_split_tiles(s) ? 1 : (tiles < want ? tiles : want);
     if (ns > kMaxSplits) ns = kMaxSplits;
     *n_splits = ns;
     *tile = it;

@@ -232,8 +232,9 @@ def test_layer_forward_equals_composed_entry_points(dim, hidden, heads, kvh, msl
         blk.close()
 
 
-# Decode positions where the split-K merge runs (more than 8 tiles of cache
-# rows); the layer tests above decode within one split.
+# Decode positions where the split-K merge runs (more tiles of cache rows than
+# one split takes: 4 tiles at hd 128 and hd 64); the layer tests above decode
+# within one split.
 SPLIT_DECODE_SHAPES = [
     # dim, hidden, heads, kv_heads, msl, prefill rows (tiles of 32 rows for hd 128, 64 for hd 64)
     (1024, 512, 8, 2, 320, 290),
