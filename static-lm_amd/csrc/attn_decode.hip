@@ -71,9 +71,30 @@ template <> struct DecodeCfg<96> { static constexpr int LPG = 8, TP = 2, NW = 4,
 template <> struct DecodeCfg<128> { static constexpr int LPG = 16, TP = 1, NW = 8, MT = 4; };
 template <> struct DecodeCfg<256> { static constexpr int LPG = 32, TP = 1, NW = 8, MT = 4; };
 
-template <int HD>
+// hd 64 has two more tilings, picked by length (decode_plan).  Per layer-step
+// (8 layers, replayed as a graph, all three interleaved in one process):
+// kShort, one position per lane group (32-row tiles, twice the splits), while
+// that stays within one merge round and one workgroup per CU: SmolLM2 shape
+// (GQA 3) at 513 / 767 rows 5.81 / 6.06 against 6.05 / 6.28 us, GQA 4 (the
+// Llama-3.2-1B layout) 6.13 / 6.51 against 6.38 / 6.78, but MHA with 16 KV
+// heads (272 workgroups) 5.77 against 5.48.  kWide, 8-wave workgroups of one
+// position per lane group (64-row tiles, one workgroup per CU, half the
+// splits), once each of its splits holds 1.5 tiles or more: GQA 4 at 3071 /
+// 8191 / 32767 rows 8.16 / 10.84 / 24.83 against 9.44 / 12.15 / 27.44 us,
+// SmolLM2 at 32767 14.42 against 14.82, MHA with 16 / 32 KV heads at 32767
+// 43.7 / 82.5 against 45.7 / 86.3.
+enum class Tiling { kBase, kShort, kWide };
+
+template <int HD, Tiling T>
+struct TilingCfg : DecodeCfg<HD> {};
+template <> struct TilingCfg<64, Tiling::kShort> { static constexpr int LPG = 8, TP = 1, NW = 4; };
+template <> struct TilingCfg<64, Tiling::kWide> { static constexpr int LPG = 8, TP = 1, NW = 8; };
+
+// Rows per tile (the positions one loop iteration of a workgroup covers).
+template <int HD, Tiling T = Tiling::kBase>
 constexpr int dec_span() {
-    return DecodeCfg<HD>::NW * (64 / DecodeCfg<HD>::LPG) * DecodeCfg<HD>::TP;
+    using C = TilingCfg<HD, T>;
+    return C::NW * (64 / C::LPG) * C::TP;
 }
 
 // Waves per CU one decode launch aims for on long sequences: two per SIMD.
@@ -629,16 +650,17 @@ __global__ __launch_bounds__(kCombineWideThreads) void decode_combine_wide_kerne
     }
 }
 
-template <int HD, int GB>
+template <int HD, int GB, Tiling T>
 hipError_t launch_t(const Shape& s, const DecodeParams& dp, hipStream_t st, hipEvent_t ev0,
                     hipEvent_t ev1) {
+    using C = TilingCfg<HD, T>;
+    const auto kern = decode_kernel<HD, GB, C::LPG, C::TP, C::NW>;
     const int groups = s.num_kv_heads * (s.kv_mul / GB);
     if (ev0 != nullptr && ev1 != nullptr)
-        hipExtLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups),
-                              dim3(64 * DecodeCfg<HD>::NW), 0, st, ev0, ev1, 0, dp);
+        hipExtLaunchKernelGGL(kern, dim3(dp.n_splits * groups), dim3(64 * C::NW), 0, st, ev0,
+                              ev1, 0, dp);
     else
-        hipLaunchKernelGGL((decode_kernel<HD, GB>), dim3(dp.n_splits * groups),
-                           dim3(64 * DecodeCfg<HD>::NW), 0, st, dp);
+        hipLaunchKernelGGL(kern, dim3(dp.n_splits * groups), dim3(64 * C::NW), 0, st, dp);
     return hipGetLastError();
 }
 
@@ -665,27 +687,50 @@ hipError_t launch_combine_t(const Shape& s, const DecodeParams& dp, hipStream_t 
     return hipGetLastError();
 }
 
-template <int HD>
-hipError_t launch_hd(const Shape& s, const DecodeParams& dp, hipStream_t st, hipEvent_t ev0,
+template <int HD, Tiling T>
+hipError_t launch_gb(const Shape& s, const DecodeParams& dp, hipStream_t st, hipEvent_t ev0,
                      hipEvent_t ev1) {
     switch (pick_gb(s.kv_mul)) {
-        case 4: return launch_t<HD, 4>(s, dp, st, ev0, ev1);
-        case 3: return launch_t<HD, 3>(s, dp, st, ev0, ev1);
-        case 2: return launch_t<HD, 2>(s, dp, st, ev0, ev1);
-        default: return launch_t<HD, 1>(s, dp, st, ev0, ev1);
+        case 4: return launch_t<HD, 4, T>(s, dp, st, ev0, ev1);
+        case 3: return launch_t<HD, 3, T>(s, dp, st, ev0, ev1);
+        case 2: return launch_t<HD, 2, T>(s, dp, st, ev0, ev1);
+        default: return launch_t<HD, 1, T>(s, dp, st, ev0, ev1);
     }
 }
 
-int decode_waves(const Shape& s) {
-    switch (s.head_dim) {
-        case 16: return DecodeCfg<16>::NW;
-        case 32: return DecodeCfg<32>::NW;
-        case 48: return DecodeCfg<48>::NW;
-        case 64: return DecodeCfg<64>::NW;
-        case 96: return DecodeCfg<96>::NW;
-        case 128: return DecodeCfg<128>::NW;
-        case 256: return DecodeCfg<256>::NW;
-        default: return kWaves;
+template <int HD>
+hipError_t launch_hd(const Shape& s, const DecodeParams& dp, Tiling t, hipStream_t st,
+                     hipEvent_t ev0, hipEvent_t ev1) {
+    if constexpr (HD == 64) {
+        if (t == Tiling::kShort) return launch_gb<HD, Tiling::kShort>(s, dp, st, ev0, ev1);
+        if (t == Tiling::kWide) return launch_gb<HD, Tiling::kWide>(s, dp, st, ev0, ev1);
+    }
+    return launch_gb<HD, Tiling::kBase>(s, dp, st, ev0, ev1);
+}
+
+// Rows per tile and waves per workgroup of a tiling.
+struct TilingDims {
+    int span, nw;
+};
+
+template <int HD, Tiling T = Tiling::kBase>
+constexpr TilingDims dims() {
+    return TilingDims{dec_span<HD, T>(), TilingCfg<HD, T>::NW};
+}
+
+TilingDims tiling_dims(int head_dim, Tiling t) {
+    switch (head_dim) {
+        case 16: return dims<16>();
+        case 32: return dims<32>();
+        case 48: return dims<48>();
+        case 64:
+            return t == Tiling::kShort  ? dims<64, Tiling::kShort>()
+                   : t == Tiling::kWide ? dims<64, Tiling::kWide>()
+                                        : dims<64>();
+        case 96: return dims<96>();
+        case 128: return dims<128>();
+        case 256: return dims<256>();
+        default: return TilingDims{64, kWaves};
     }
 }
 
@@ -702,46 +747,60 @@ int decode_one_split_tiles(const Shape& s) {
     }
 }
 
-int decode_span(const Shape& s) {
-    switch (s.head_dim) {
-        case 16: return dec_span<16>();
-        case 32: return dec_span<32>();
-        case 48: return dec_span<48>();
-        case 64: return dec_span<64>();
-        case 96: return dec_span<96>();
-        case 128: return dec_span<128>();
-        case 256: return dec_span<256>();
-        default: return 64;
+struct DecodePlan {
+    int n_splits, tile;
+    Tiling tiling;
+    int tiles, want;  // tiles of the sequence; splits that fill the CUs
+};
+
+int decode_groups_of(const Shape& s) { return s.num_kv_heads * (s.kv_mul / pick_gb(s.kv_mul)); }
+
+// As many splits as there are tiles, up to two waves per SIMD (for 8-wave
+// workgroups one per CU: a few workgroups more than CUs double some CUs up
+// and measured 20-30% slower) and kMaxSplits.  Below that the kernel is
+// latency-bound and every tile a split walks costs about one memory round
+// trip, so one tile per split wins (Llama-3-8B shape at 4096 rows: 15.0 us
+// with 32 splits against 17.4 us with 16; SmolLM2 at 768 rows: 10.8 us with
+// 12 splits against 13.0 us with one).  Up to DecodeCfg::MT tiles (2-4 by
+// head_dim) the merge launch costs more than it saves, and a single split
+// writes the output directly.  hd 64 then picks among its tilings (see
+// Tiling).  A pure function of seq_len, the shape and the CU count, so the
+// launch finds the same tiling and results reproduce run to run on a device.
+DecodePlan decode_plan(const Shape& s, int seq_len) {
+    const int groups = decode_groups_of(s);
+    auto plan = [&](Tiling t) {
+        const TilingDims d = tiling_dims(s.head_dim, t);
+        const int wgs = kWavesPerCu * s.cus / d.nw;
+        const int want = groups >= wgs ? 1 : wgs / groups;
+        const int tiles = (seq_len + d.span - 1) / d.span;
+        int ns = tiles < want ? tiles : want;
+        if (ns > kMaxSplits) ns = kMaxSplits;
+        return DecodePlan{ns, d.span, t, tiles, want};
+    };
+    DecodePlan base = plan(Tiling::kBase);
+    if (base.tiles <= decode_one_split_tiles(s)) {
+        base.n_splits = 1;
+        return base;
     }
+    if (s.head_dim == 64) {
+        const DecodePlan sh = plan(Tiling::kShort);
+        if (sh.n_splits <= kCombineRound && sh.n_splits * groups <= s.cus) return sh;
+        const DecodePlan wide = plan(Tiling::kWide);
+        if (2 * base.tiles >= 3 * wide.want) return wide;
+    }
+    return base;
 }
 
 }  // namespace
 
-int decode_groups(const Shape& s) { return s.num_kv_heads * (s.kv_mul / pick_gb(s.kv_mul)); }
+int decode_groups(const Shape& s) { return decode_groups_of(s); }
 
 int decode_max_splits() { return kMaxSplits; }
 
 void decode_split_policy(const Shape& s, int seq_len, int* n_splits, int* tile) {
-    // As many splits as there are tiles, up to two waves per SIMD (for
-    // 8-wave workgroups one per CU: a few workgroups more than CUs double
-    // some CUs up and measured 20-30% slower) and kMaxSplits.  Below that
-    // the kernel is latency-bound and every tile a split walks costs about
-    // one memory round trip, so one tile per split wins (Llama-3-8B shape at
-    // 4096 rows: 15.0 us with 32 splits against 17.4 us with 16; SmolLM2 at
-    // 768 rows: 10.8 us with 12 splits against 13.0 us with one).  Up to
-    // DecodeCfg::MT tiles (2-4 by head_dim) the merge launch costs more than
-    // it saves, and a single split writes the output directly.  A pure
-    // function of seq_len, the shape and the CU count, so results reproduce
-    // run to run on a device.
-    const int it = decode_span(s);
-    const int groups = decode_groups(s);
-    const int wgs = kWavesPerCu * s.cus / decode_waves(s);
-    const int want = groups >= wgs ? 1 : wgs / groups;
-    const int tiles = (seq_len + it - 1) / it;
-    int ns = tiles <= decode_one_split_tiles(s) ? 1 : (tiles < want ? tiles : want);
-    if (ns > kMaxSplits) ns = kMaxSplits;
-    *n_splits = ns;
-    *tile = it;
+    const DecodePlan pl = decode_plan(s, seq_len);
+    *n_splits = pl.n_splits;
+    *tile = pl.tile;
 }
 
 static DecodeParams decode_params(const Shape& s, const DecodeArgs& a) {
@@ -774,14 +833,15 @@ hipError_t launch_decode(const Shape& s, const DecodeArgs& a, hipStream_t st) {
     // whenever it appends)
     if (a.k_new != nullptr && (a.cos_t == nullptr || a.sin_t == nullptr || a.v_new == nullptr))
         return hipErrorInvalidValue;
+    const Tiling t = decode_plan(s, a.pos + 1).tiling;
     switch (s.head_dim) {
-        case 16: return launch_hd<16>(s, dp, st, a.ev_start, a.ev_stop);
-        case 32: return launch_hd<32>(s, dp, st, a.ev_start, a.ev_stop);
-        case 48: return launch_hd<48>(s, dp, st, a.ev_start, a.ev_stop);
-        case 64: return launch_hd<64>(s, dp, st, a.ev_start, a.ev_stop);
-        case 96: return launch_hd<96>(s, dp, st, a.ev_start, a.ev_stop);
-        case 128: return launch_hd<128>(s, dp, st, a.ev_start, a.ev_stop);
-        case 256: return launch_hd<256>(s, dp, st, a.ev_start, a.ev_stop);
+        case 16: return launch_hd<16>(s, dp, t, st, a.ev_start, a.ev_stop);
+        case 32: return launch_hd<32>(s, dp, t, st, a.ev_start, a.ev_stop);
+        case 48: return launch_hd<48>(s, dp, t, st, a.ev_start, a.ev_stop);
+        case 64: return launch_hd<64>(s, dp, t, st, a.ev_start, a.ev_stop);
+        case 96: return launch_hd<96>(s, dp, t, st, a.ev_start, a.ev_stop);
+        case 128: return launch_hd<128>(s, dp, t, st, a.ev_start, a.ev_stop);
+        case 256: return launch_hd<256>(s, dp, t, st, a.ev_start, a.ev_stop);
         default: return hipErrorInvalidValue;
     }
 }

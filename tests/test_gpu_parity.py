@@ -559,24 +559,23 @@ def test_decode_split_tiles_across_shapes(dim, heads, kv_heads):
     the last row of the last split's tile, and a row inside another split's.
     """
     with P.AttentionContext(dim, heads, kv_heads, 16, 1) as probe:
-        cap, tile = probe.decode_splits(1 << 24)
-    msl = 2 * cap * tile + 2 * tile
+        cap, tile = probe.decode_splits(1 << 24)  # the tiling of long sequences
+    msl = 3 * cap * tile + 2 * tile
     cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, 1e4)
     kvd = cfg.kv_dim
     om = orc.OracleModel(cfg)
     with P.AttentionContext(dim, heads, kv_heads, msl, 1) as ctx:
         picks = {}
         for p in range(msl - 1):
-            ns, t = ctx.decode_splits(p + 1)
-            assert t == tile
+            ns, t = ctx.decode_splits(p + 1)  # hd 64 picks its tile by length
             if ns == 1:
                 continue
             picks.setdefault("shortest split sequence", p)
-            if ns < p // tile + 1:  # past the cap
-                owner, row = (p // tile) % ns, p % tile
+            if ns < p // t + 1:  # past the cap
+                owner, row = (p // t) % ns, p % t
                 for key, at in (("split 0 tile start", (0, 0)), ("split 1 tile start", (1, 0)),
-                                ("last split, last row", (ns - 1, tile - 1)),
-                                ("another split", (min(3, ns - 1), 5 % tile))):
+                                ("last split, last row", (ns - 1, t - 1)),
+                                ("another split", (min(3, ns - 1), 5 % t))):
                     if (owner, row) == at:
                         picks.setdefault(key, p)
         assert len(picks) == 5, picks
@@ -608,8 +607,8 @@ MANY_SPLITS = [
     ((128, 8, 2), (256,)),           # hd 16
     ((256, 8, 2), (200,)),           # hd 32
     ((288, 6, 6), (85,)),            # hd 48 MHA: the policy's cap
-    ((576, 9, 3), (48, 65, 170)),    # hd 64 GQA 3 (SmolLM2): 170 is its cap
-    ((2048, 32, 8), (64,)),          # hd 64 GQA 4
+    ((576, 9, 3), (48, 65, 85)),     # hd 64 GQA 3 (SmolLM2)
+    ((2048, 32, 8), (40,)),          # hd 64 GQA 4
     ((768, 8, 8), (64,)),            # hd 96: 128 threads per row
     ((1024, 8, 2), (128,)),          # hd 128 GQA 4
     ((1024, 4, 1), (128, 129, 256)), # hd 256: the wide merge's limit, then rounds
@@ -623,9 +622,18 @@ def test_decode_many_splits_against_oracle(dim, heads, kv_heads, target):
     output against the oracle, the appended K/V row bit for bit, and a
     second call giving the same bits."""
     with P.AttentionContext(dim, heads, kv_heads, 16, 1) as probe:
-        cap, tile = probe.decode_splits(1 << 24)
-    assert target <= cap, (target, cap)
-    p = target * tile - tile // 3 - 1  # the last tile holds 2/3 of its rows
+        run = []
+        for n in range(1, 1 << 18):  # the first run of lengths with `target` splits
+            ns_n, t_n = probe.decode_splits(n)
+            if ns_n == target:
+                run.append((n, t_n))
+            elif run:
+                break
+    assert run, f"no length gives {target} splits"
+    n, tile = run[len(run) // 2]
+    if n % tile == 0 and len(run) > 1:  # ragged: the last tile not full
+        n, tile = run[len(run) // 2 - 1]
+    p = n - 1
     msl = p + 1
     cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, 1e4)
     kvd = cfg.kv_dim
@@ -647,6 +655,111 @@ def test_decode_many_splits_against_oracle(dim, heads, kv_heads, target):
         assert_bitwise(ctx.kv_read(0, 0, p, 1), om.k_cache(0)[p:p + 1], f"K row {p}")
         assert_bitwise(ctx.kv_read(0, 1, p, 1), om.v_cache(0)[p:p + 1], f"V row {p}")
         assert_bitwise(ctx.decode(0, p, q1, k1, v1), g, f"second decode at {p}")
+
+
+def pick_gb(kv_mul):
+    return 4 if kv_mul % 4 == 0 else 3 if kv_mul % 3 == 0 else 2 if kv_mul % 2 == 0 else 1
+
+
+def hd64_plan(seq_len, heads, kv_heads, cus):
+    """The decode split policy for head_dim 64, restated: (n_splits, tile rows,
+    tiling).  Tilings: base (64-row tiles of 4-wave workgroups), short
+    (32-row tiles of 4 waves) and wide (64-row tiles of 8 waves); each fills
+    the CUs with up to 8 waves per CU.  One split up to 4 base tiles; short
+    while its splits stay within 32 and one workgroup per CU; wide once the
+    base tiles reach 1.5 times its split count."""
+    kv_mul = heads // kv_heads
+    groups = kv_heads * (kv_mul // pick_gb(kv_mul))
+
+    def plan(span, nw):
+        wgs = 8 * cus // nw
+        want = 1 if groups >= wgs else wgs // groups
+        tiles = -(-seq_len // span)
+        return min(tiles, want, 1024), tiles, want
+
+    ns_b, tiles_b, _ = plan(64, 4)
+    if tiles_b <= 4:
+        return 1, 64, "base"
+    ns_s, _, _ = plan(32, 4)
+    if ns_s <= 32 and ns_s * groups <= cus:
+        return ns_s, 32, "short"
+    ns_w, _, want_w = plan(64, 8)
+    if 2 * tiles_b >= 3 * want_w:
+        return ns_w, 64, "wide"
+    return ns_b, 64, "base"
+
+
+HD64_SHAPES = [
+    (576, 9, 3),      # SmolLM2-135M: GQA 3
+    (2048, 32, 8),    # Llama-3.2-1B layout: GQA 4
+    (1024, 16, 8),    # GQA 2
+    (1024, 16, 16),   # MHA, 16 KV heads (short would take 272 workgroups)
+    (2048, 32, 32),   # MHA, 32 KV heads
+    (256, 4, 4),      # MHA, 4 KV heads (the reference's synthetic model shape)
+]
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads", HD64_SHAPES)
+def test_decode_hd64_tilings_against_oracle(dim, heads, kv_heads):
+    """hd 64 picks its tiling by length.  The policy at every length up to
+    past the wide tiling's start against hd64_plan; then decode with append
+    at the first and last length of each run of one (tiling, split count)
+    change and at a ragged length inside each tiling, against the oracle, with
+    the appended K/V rows bit for bit."""
+    torch = pytest.importorskip("torch")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    runs = []  # [first length, last length, (ns, tile, tiling)]
+    with P.AttentionContext(dim, heads, kv_heads, 16, 1) as probe:
+        n = 1
+        while True:
+            want = hd64_plan(n, heads, kv_heads, cus)
+            got = probe.decode_splits(n)
+            assert got == want[:2], (n, got, want)
+            if runs and runs[-1][2] == want:
+                runs[-1][1] = n
+            else:
+                runs.append([n, n, want])
+            if want[2] == "wide" and n - runs[-1][0] > 300:
+                break
+            n += 1
+    tilings = {r[2][2] for r in runs}
+    assert {"base", "wide"} <= tilings, tilings
+    picks = set()
+    for first, last, _ in runs:
+        picks |= {first, last}
+    for t in tilings:
+        r = max((r for r in runs if r[2][2] == t), key=lambda r: r[1] - r[0])
+        mid = (r[0] + r[1]) // 2
+        picks.add(mid if mid % r[2][1] else mid + 1 if mid < r[1] else mid - 1)
+    # the decode positions p = length - 1; runs of one split count change often
+    # at short lengths, so keep the transitions between tilings and a sample
+    keys = sorted(picks)
+    trans = set()
+    for a, b in zip(runs, runs[1:]):
+        if a[2][2] != b[2][2]:
+            trans |= {a[1], b[0]}
+    sample = sorted(trans | set(keys[::max(1, len(keys) // 12)]) | {keys[-1]})
+    msl = sample[-1]
+    cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, 1e4)
+    kvd = cfg.kv_dim
+    om = orc.OracleModel(cfg)
+    log(f"hd 64 {heads}/{kv_heads}: tilings {[(r[0], r[1], r[2]) for r in runs if r[2][2] != 'base' or r[2][0] == 1][:6]} ...; lengths {sample}")
+    with P.AttentionContext(dim, heads, kv_heads, msl, 1) as ctx:
+        top = msl - 1
+        kr = gen([97, dim], (top, kvd))
+        vr = gen([98, dim], (top, kvd))
+        ctx.kv_write(0, 0, 0, kr)
+        ctx.kv_write(0, 1, 0, vr)
+        om.k_cache(0)[:top] = kr
+        om.v_cache(0)[:top] = vr
+        for n in sample:
+            p = n - 1
+            q1, k1, v1 = gen([99, p], dim), gen([100, p], kvd), gen([101, p], kvd)
+            g = ctx.decode(0, p, q1, k1, v1)
+            r = om.decode(0, p, q1, k1, v1)
+            assert_close(g, r, what=f"decode at {p} ({hd64_plan(n, heads, kv_heads, cus)})")
+            assert_bitwise(ctx.kv_read(0, 0, p, 1), om.k_cache(0)[p:p + 1], f"K row {p}")
+            assert_bitwise(ctx.kv_read(0, 1, p, 1), om.v_cache(0)[p:p + 1], f"V row {p}")
 
 
 def test_calibration_helpers_report_plausible_rates():
