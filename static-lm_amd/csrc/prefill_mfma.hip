@@ -148,8 +148,14 @@ constexpr int prefill_waves_per_simd() {
 // walked by KSP SIMDs instead of one.  (Splitting keys among the waves of a workgroup that
 // already has a wave on every SIMD gains nothing: the per-SIMD MFMA work of
 // the heaviest block stays the same.)
+//
+// PAIR (with QS = 2): the workgroup's two query blocks are i and n_qb-1-i
+// (16-row blocks), so every workgroup has the same causal work, and the
+// waves are numbered key split first, then head, then block: the waves of one
+// SIMD hold the same head and key split of the heavy and the light block,
+// and every SIMD gets the same share.
 template <int HD, int HW, int QS, int NQT, int kKT = 32, int NB = 1, bool PRIO = false,
-          bool DMA = false, int KSP = 1>
+          bool DMA = false, int KSP = 1, bool PAIR = false>
 __global__ __launch_bounds__(64 * HW * QS * KSP,
                              (DMA ? 4 : prefill_waves_per_simd<HD, HW>())) void
 prefill_mfma_kernel(PrefillParams p) {
@@ -194,22 +200,33 @@ prefill_mfma_kernel(PrefillParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    const int hw = wave % HW;
-    const int qs = (wave / HW) % QS;
-    const int kspl = wave / NWS;  // key split
+    static_assert(!PAIR || (QS == 2 && NQT == 1 && !DMA), "pairs: two 16-row blocks");
+    const int hw = PAIR ? (wave / KSP) % HW : wave % HW;
+    const int qs = PAIR ? wave / (KSP * HW) : (wave / HW) % QS;
+    const int kspl = PAIR ? wave % KSP : wave / NWS;  // key split
 
     // blockIdx.x = query block * head groups + head group: consecutive
     // workgroups go round-robin to the 8 XCDs, so with 8 head groups each XCD's
     // L2 serves one KV head's K/V; longest causal ranges are launched first.
-    const int n_qb = (p.n + QB - 1) / QB;
+    // Pairs: blockIdx.x = pair * head groups + head group, pair i holding
+    // 16-row blocks n_qb-1-i (qs 0) and i (qs 1); with n_qb odd the middle
+    // pair's second block is the first's, and its waves hold no rows.
+    const int n_qb = PAIR ? (p.n + QPW - 1) / QPW : (p.n + QB - 1) / QB;
     const int n_hg = p.num_heads / HW;
     const int hg = (int)blockIdx.x % n_hg;
-    const int qb = n_qb - 1 - (int)blockIdx.x / n_hg;
     const int head = hg * HW + hw;
     const int g = (hg * HW) / p.kv_mul;
-    const int q0 = qb * QB + qs * QPW;  // first query row of this wave
-    const int wg_rows = min(p.n - qb * QB, QB);
-    const int kv_len = p.start + qb * QB + wg_rows;  // keys 0..kv_len-1
+    int q0, kv_len;  // first query row of this wave; keys 0..kv_len-1
+    if constexpr (PAIR) {
+        const int pi = (int)blockIdx.x / n_hg;
+        const int heavy = n_qb - 1 - pi;
+        q0 = qs == 0 ? heavy * QPW : pi < heavy ? pi * QPW : p.n;
+        kv_len = p.start + min(p.n, (heavy + 1) * QPW);
+    } else {
+        const int qb = n_qb - 1 - (int)blockIdx.x / n_hg;
+        q0 = qb * QB + qs * QPW;
+        kv_len = p.start + qb * QB + min(p.n - qb * QB, QB);
+    }
     const int n_tiles = (kv_len + kKT - 1) / kKT;
     const int wave_rows = max(0, min(QPW, p.n - q0));
     const int wave_last_pos = p.start + q0 + wave_rows - 1;
@@ -606,7 +623,7 @@ prefill_mfma_kernel(PrefillParams p) {
         static_assert((KSP - 1) * NWS * 64 * NR <= NSLOT * kKT * (LDK + LDV),
                       "the merge fits the tile LDS");
         __syncthreads();  // every wave is done with the tiles
-        const int ws = wave % NWS;
+        const int ws = qs * HW + hw;  // the wave's place in its key split's set
         if (kspl > 0) {
             float* dst = s_tiles + ((kspl - 1) * NWS + ws) * NR * 64 + lane;
             int r = 0;
@@ -705,17 +722,17 @@ Tiling pick_tiling(int kv_mul) {
     return {1, 4};
 }
 
-template <int HD, int HW, int QS, int KSP>
+template <int HD, int HW, int QS, int KSP, bool PAIR = false>
 hipError_t launch_t(const Shape& s, const PrefillParams& pp, hipStream_t st) {
     // 16 query rows per wave: measured on MI355X (hd 128, 4096 rows) 57% of
     // the fp32 MFMA peak against 47% with 32 rows per wave, because the lower
     // register count (~160 VGPRs) allows three waves per SIMD
     constexpr int NQT = 1;
     constexpr int QB = 16 * NQT * QS;
-    const int n_qb = (pp.n + QB - 1) / QB;
+    const int n_qb = PAIR ? ((pp.n + 15) / 16 + 1) / 2 : (pp.n + QB - 1) / QB;
     const dim3 grid(n_qb * (s.num_heads / HW));
-    hipLaunchKernelGGL((prefill_mfma_kernel<HD, HW, QS, NQT, 32, 1, false, false, KSP>), grid,
-                       dim3(64 * HW * QS * KSP), 0, st, pp);
+    hipLaunchKernelGGL((prefill_mfma_kernel<HD, HW, QS, NQT, 32, 1, false, false, KSP, PAIR>),
+                       grid, dim3(64 * HW * QS * KSP), 0, st, pp);
     return hipGetLastError();
 }
 
@@ -738,6 +755,19 @@ hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
                                dim3(n_qb * (s.num_heads / 4)), dim3(512), 0, st, pp);
             return hipGetLastError();
         }
+        // Short prefills whose head-group tiling gives at most one workgroup
+        // per CU run one wave per SIMD, and the heaviest causal block sets
+        // the time (its tiles in series: 16 at 512 rows, against 8.5 on
+        // average).  Pairs of blocks i and n_qb-1-i, two heads and two key
+        // splits per workgroup give every SIMD the same share.  Measured for
+        // the Llama-3-8B shape (interleaved, per call): 256 rows 25.6 against
+        // 28.2 us, 512 rows 39.9 against 49.7, 512 rows at start 1000 111.2
+        // against 125.6; 1024 rows (two workgroups per CU) even; 2048 / 3072
+        // rows 368 / 785 against 301 / 607 us (158 VGPRs: one 8-wave workgroup
+        // per CU against three 4-wave ones); below 256 rows 13% slower.
+        const long wgs = (long)((pp.n + 16 * t.qs - 1) / (16 * t.qs)) * (s.num_heads / t.hw);
+        if (s.kv_mul % 2 == 0 && pp.n >= 256 && wgs <= s.cus)
+            return launch_t<128, 2, 2, 2, true>(s, pp, st);
     }
     // Short prefills, head_dim <= 64: when the head-group tiling gives fewer
     // than two workgroups per CU, one head and one 16-row query block per

@@ -193,6 +193,47 @@ def test_llama3_shape_short_prefill_every_row(start, n):
         assert_close(g, ref, what=f"prefill of {n} rows at {start}")
 
 
+def takes_paired_blocks(dim, heads, kv_heads, n, cus=256):
+    """hd 128 prefills of at least 256 rows whose head-group tiling gives at
+    most one workgroup per CU take the paired-block kernel (blocks i and
+    n_qb-1-i, two heads, two key splits) when kv_mul is even."""
+    hd = dim // heads
+    kv_mul = heads // kv_heads
+    hw, qs = (4, 1) if kv_mul % 4 == 0 else (3, 1) if kv_mul % 3 == 0 else \
+        (2, 2) if kv_mul % 2 == 0 else (1, 4)
+    wgs = -(-n // (16 * qs)) * (heads // hw)
+    return hd == 128 and kv_mul % 2 == 0 and n >= 256 and wgs <= cus
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads,start,n", [
+    (4096, 32, 8, 0, 256),     # 16 blocks: 8 pairs
+    (4096, 32, 8, 0, 300),     # 19 blocks: the middle pair's second block is its first
+    (4096, 32, 8, 37, 471),    # unaligned start and a partial last block
+    (4096, 32, 8, 1000, 512),  # a long prefix: every block's keys span 48 tiles
+    (2048, 16, 2, 0, 777),     # kv_mul 8: two head pairs per KV head, 49 blocks
+    (1024, 8, 4, 13, 1500),    # kv_mul 2
+])
+def test_prefill_paired_blocks_every_row(dim, heads, kv_heads, start, n):
+    # every row against the oracle, K/V rows bit for bit
+    assert takes_paired_blocks(dim, heads, kv_heads, n)
+    rows = start + n
+    cfg = orc.Cfg(dim, heads, kv_heads, rows, 1, 5e5)
+    q = gen([102, start, n], (rows, dim))
+    k = gen([103, start, n], (rows, cfg.kv_dim))
+    v = gen([104, start, n], (rows, cfg.kv_dim))
+    om = orc.OracleModel(cfg)
+    with P.AttentionContext(dim, heads, kv_heads, rows, 1, 5e5) as ctx:
+        log(f"paired-block prefill {heads}/{kv_heads} heads: {n} rows at start {start}")
+        if start:
+            ctx.prefill(0, 0, q[:start], k[:start], v[:start])
+            om.append(0, 0, k[:start], v[:start])
+        g = ctx.prefill(0, start, q[start:], k[start:], v[start:])
+        ref = om.prefill(0, start, q[start:], k[start:], v[start:])
+        assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
+        assert_close(g, ref, what=f"prefill of {n} rows at {start}")
+
+
 def test_long_context_decode_131072():
     w = WORKLOADS["c5"]
     cfg = w.cfg()
