@@ -71,24 +71,37 @@ template <> struct DecodeCfg<96> { static constexpr int LPG = 8, TP = 2, NW = 4,
 template <> struct DecodeCfg<128> { static constexpr int LPG = 16, TP = 1, NW = 8, MT = 4; };
 template <> struct DecodeCfg<256> { static constexpr int LPG = 32, TP = 1, NW = 8, MT = 4; };
 
-// hd 64 has two more tilings, picked by length (decode_plan).  Per layer-step
-// (8 layers, replayed as a graph, all three interleaved in one process):
-// kShort, one position per lane group (32-row tiles, twice the splits), while
-// that stays within one merge round and one workgroup per CU: SmolLM2 shape
-// (GQA 3) at 513 / 767 rows 5.81 / 6.06 against 6.05 / 6.28 us, GQA 4 (the
-// Llama-3.2-1B layout) 6.13 / 6.51 against 6.38 / 6.78, but MHA with 16 KV
-// heads (272 workgroups) 5.77 against 5.48.  kWide, 8-wave workgroups of one
-// position per lane group (64-row tiles, one workgroup per CU, half the
-// splits), once each of its splits holds 1.5 tiles or more: GQA 4 at 3071 /
-// 8191 / 32767 rows 8.16 / 10.84 / 24.83 against 9.44 / 12.15 / 27.44 us,
-// SmolLM2 at 32767 14.42 against 14.82, MHA with 16 / 32 KV heads at 32767
-// 43.7 / 82.5 against 45.7 / 86.3.
+// Two more tilings, picked by length (decode_plan).  Per layer-step (8
+// layers, replayed as a graph, the tilings interleaved in one process):
+// kShort, one position per lane group (half the tile, twice the splits), for
+// the head dims whose base tiling takes two (hd 16-96), while that stays
+// within one merge round and one workgroup per CU: at 1023 rows hd 16 / 32 /
+// 48 / 64 / 96 with GQA 4 7.16 / 7.20 / 7.85 / 6.60 / 7.55 us against 7.57 /
+// 8.00 / 8.87 / 6.79 / 7.85, the SmolLM2 shape (hd 64, GQA 3) at 513 / 767
+// rows 5.81 / 6.06 against 6.05 / 6.28, but MHA with 16 KV heads at 513 rows
+// (272 workgroups) 5.77 against 5.48.  kWide, 8-wave workgroups of one
+// position per lane group (one workgroup per CU, half the splits), for hd 64
+// and 96 once each of its splits holds 1.5 tiles or more: GQA 4 at 8191 rows
+// 10.84 / 13.87 us against 12.15 / 15.81 (hd 64 / 96), hd 64 at 32767 24.83
+// against 27.44 and MHA with 16 / 32 KV heads 43.7 / 82.5 against 45.7 /
+// 86.3; at hd 16, 32 and 48 it lost or tied (hd 48 GQA 4 at 8191 rows 13.36
+// against 13.46, Stories-15M shape 12.18 against 11.25).
 enum class Tiling { kBase, kShort, kWide };
 
 template <int HD, Tiling T>
 struct TilingCfg : DecodeCfg<HD> {};
-template <> struct TilingCfg<64, Tiling::kShort> { static constexpr int LPG = 8, TP = 1, NW = 4; };
-template <> struct TilingCfg<64, Tiling::kWide> { static constexpr int LPG = 8, TP = 1, NW = 8; };
+template <int HD>
+struct TilingCfg<HD, Tiling::kShort> {
+    static constexpr int LPG = DecodeCfg<HD>::LPG, TP = 1, NW = DecodeCfg<HD>::NW;
+};
+template <int HD>
+struct TilingCfg<HD, Tiling::kWide> {
+    static constexpr int LPG = DecodeCfg<HD>::LPG, TP = 1, NW = 8;
+};
+template <int HD>
+constexpr bool has_short() { return DecodeCfg<HD>::TP == 2; }
+template <int HD>
+constexpr bool has_wide() { return HD == 64 || HD == 96; }
 
 // Rows per tile (the positions one loop iteration of a workgroup covers).
 template <int HD, Tiling T = Tiling::kBase>
@@ -701,10 +714,10 @@ hipError_t launch_gb(const Shape& s, const DecodeParams& dp, hipStream_t st, hip
 template <int HD>
 hipError_t launch_hd(const Shape& s, const DecodeParams& dp, Tiling t, hipStream_t st,
                      hipEvent_t ev0, hipEvent_t ev1) {
-    if constexpr (HD == 64) {
+    if constexpr (has_short<HD>())
         if (t == Tiling::kShort) return launch_gb<HD, Tiling::kShort>(s, dp, st, ev0, ev1);
+    if constexpr (has_wide<HD>())
         if (t == Tiling::kWide) return launch_gb<HD, Tiling::kWide>(s, dp, st, ev0, ev1);
-    }
     return launch_gb<HD, Tiling::kBase>(s, dp, st, ev0, ev1);
 }
 
@@ -713,26 +726,36 @@ struct TilingDims {
     int span, nw;
 };
 
-template <int HD, Tiling T = Tiling::kBase>
-constexpr TilingDims dims() {
+template <int HD, Tiling T>
+constexpr TilingDims dims_t() {
     return TilingDims{dec_span<HD, T>(), TilingCfg<HD, T>::NW};
+}
+
+// The tiling's dims (the base tiling's where the head dim has no such tiling).
+template <int HD>
+TilingDims dims(Tiling t) {
+    if constexpr (has_short<HD>())
+        if (t == Tiling::kShort) return dims_t<HD, Tiling::kShort>();
+    if constexpr (has_wide<HD>())
+        if (t == Tiling::kWide) return dims_t<HD, Tiling::kWide>();
+    return dims_t<HD, Tiling::kBase>();
 }
 
 TilingDims tiling_dims(int head_dim, Tiling t) {
     switch (head_dim) {
-        case 16: return dims<16>();
-        case 32: return dims<32>();
-        case 48: return dims<48>();
-        case 64:
-            return t == Tiling::kShort  ? dims<64, Tiling::kShort>()
-                   : t == Tiling::kWide ? dims<64, Tiling::kWide>()
-                                        : dims<64>();
-        case 96: return dims<96>();
-        case 128: return dims<128>();
-        case 256: return dims<256>();
+        case 16: return dims<16>(t);
+        case 32: return dims<32>(t);
+        case 48: return dims<48>(t);
+        case 64: return dims<64>(t);
+        case 96: return dims<96>(t);
+        case 128: return dims<128>(t);
+        case 256: return dims<256>(t);
         default: return TilingDims{64, kWaves};
     }
 }
+
+bool tiling_short(int head_dim) { return head_dim <= 96; }  // has_short<HD>()
+bool tiling_wide(int head_dim) { return head_dim == 64 || head_dim == 96; }
 
 int decode_one_split_tiles(const Shape& s) {
     switch (s.head_dim) {
@@ -763,7 +786,7 @@ int decode_groups_of(const Shape& s) { return s.num_kv_heads * (s.kv_mul / pick_
 // with 32 splits against 17.4 us with 16; SmolLM2 at 768 rows: 10.8 us with
 // 12 splits against 13.0 us with one).  Up to DecodeCfg::MT tiles (2-4 by
 // head_dim) the merge launch costs more than it saves, and a single split
-// writes the output directly.  hd 64 then picks among its tilings (see
+// writes the output directly.  hd 16-96 then pick among their tilings (see
 // Tiling).  A pure function of seq_len, the shape and the CU count, so the
 // launch finds the same tiling and results reproduce run to run on a device.
 DecodePlan decode_plan(const Shape& s, int seq_len) {
@@ -782,9 +805,11 @@ DecodePlan decode_plan(const Shape& s, int seq_len) {
         base.n_splits = 1;
         return base;
     }
-    if (s.head_dim == 64) {
+    if (tiling_short(s.head_dim)) {
         const DecodePlan sh = plan(Tiling::kShort);
         if (sh.n_splits <= kCombineRound && sh.n_splits * groups <= s.cus) return sh;
+    }
+    if (tiling_wide(s.head_dim)) {
         const DecodePlan wide = plan(Tiling::kWide);
         if (2 * base.tiles >= 3 * wide.want) return wide;
     }

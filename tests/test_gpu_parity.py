@@ -650,7 +650,7 @@ MANY_SPLITS = [
     ((288, 6, 6), (85,)),            # hd 48 MHA: the policy's cap
     ((576, 9, 3), (48, 65, 85)),     # hd 64 GQA 3 (SmolLM2)
     ((2048, 32, 8), (40,)),          # hd 64 GQA 4
-    ((768, 8, 8), (64,)),            # hd 96: 128 threads per row
+    ((768, 8, 8), (40,)),            # hd 96: 128 threads per row
     ((1024, 8, 2), (128,)),          # hd 128 GQA 4
     ((1024, 4, 1), (128, 129, 256)), # hd 256: the wide merge's limit, then rounds
 ]
@@ -702,78 +702,103 @@ def pick_gb(kv_mul):
     return 4 if kv_mul % 4 == 0 else 3 if kv_mul % 3 == 0 else 2 if kv_mul % 2 == 0 else 1
 
 
-def hd64_plan(seq_len, heads, kv_heads, cus):
-    """The decode split policy for head_dim 64, restated: (n_splits, tile rows,
-    tiling).  Tilings: base (64-row tiles of 4-wave workgroups), short
-    (32-row tiles of 4 waves) and wide (64-row tiles of 8 waves); each fills
-    the CUs with up to 8 waves per CU.  One split up to 4 base tiles; short
-    while its splits stay within 32 and one workgroup per CU; wide once the
-    base tiles reach 1.5 times its split count."""
+# the decode kernel's base tiling per head dim: lanes per position, positions
+# per lane group and iteration, waves per workgroup, and the most tiles that
+# still run as one split
+DECODE_BASE = {16: (2, 2, 4, 3), 32: (4, 2, 4, 3), 48: (4, 2, 4, 2), 64: (8, 2, 4, 4),
+               96: (8, 2, 4, 3), 128: (16, 1, 8, 4), 256: (32, 1, 8, 4)}
+
+
+def decode_plan(seq_len, heads, kv_heads, hd, cus):
+    """The decode split policy, restated: (n_splits, tile rows, tiling).  A
+    tiling fills the CUs with up to 8 waves per CU, one tile per split.  One
+    split up to the head dim's tile limit; then, where the base tiling takes
+    two positions per lane group (hd <= 96), the short tiling (one position)
+    while its splits stay within 32 and one workgroup per CU; for hd 64 and
+    96 the wide tiling (8-wave workgroups, one position) once the base tiles
+    reach 1.5 times its split count; else the base tiling."""
+    lpg, tp, nw, mt = DECODE_BASE[hd]
     kv_mul = heads // kv_heads
     groups = kv_heads * (kv_mul // pick_gb(kv_mul))
 
-    def plan(span, nw):
-        wgs = 8 * cus // nw
+    def plan(tp_, nw_):
+        span = nw_ * (64 // lpg) * tp_
+        wgs = 8 * cus // nw_
         want = 1 if groups >= wgs else wgs // groups
         tiles = -(-seq_len // span)
-        return min(tiles, want, 1024), tiles, want
+        return min(tiles, want, 1024), span, tiles, want
 
-    ns_b, tiles_b, _ = plan(64, 4)
-    if tiles_b <= 4:
-        return 1, 64, "base"
-    ns_s, _, _ = plan(32, 4)
-    if ns_s <= 32 and ns_s * groups <= cus:
-        return ns_s, 32, "short"
-    ns_w, _, want_w = plan(64, 8)
-    if 2 * tiles_b >= 3 * want_w:
-        return ns_w, 64, "wide"
-    return ns_b, 64, "base"
+    ns_b, span_b, tiles_b, _ = plan(tp, nw)
+    if tiles_b <= mt:
+        return 1, span_b, "base"
+    if tp == 2:
+        ns_s, span_s, _, _ = plan(1, nw)
+        if ns_s <= 32 and ns_s * groups <= cus:
+            return ns_s, span_s, "short"
+    if hd in (64, 96):
+        ns_w, span_w, _, want_w = plan(1, 8)
+        if 2 * tiles_b >= 3 * want_w:
+            return ns_w, span_w, "wide"
+    return ns_b, span_b, "base"
 
 
-HD64_SHAPES = [
-    (576, 9, 3),      # SmolLM2-135M: GQA 3
-    (2048, 32, 8),    # Llama-3.2-1B layout: GQA 4
-    (1024, 16, 8),    # GQA 2
-    (1024, 16, 16),   # MHA, 16 KV heads (short would take 272 workgroups)
-    (2048, 32, 32),   # MHA, 32 KV heads
-    (256, 4, 4),      # MHA, 4 KV heads (the reference's synthetic model shape)
+TILING_SHAPES = [
+    (576, 9, 3),      # hd 64, SmolLM2-135M: GQA 3
+    (2048, 32, 8),    # hd 64, the Llama-3.2-1B layout: GQA 4
+    (1024, 16, 8),    # hd 64, GQA 2
+    (1024, 16, 16),   # hd 64, MHA with 16 KV heads (short would take 272 workgroups)
+    (2048, 32, 32),   # hd 64, MHA with 32 KV heads
+    (256, 4, 4),      # hd 64, MHA with 4 KV heads (the reference's synthetic model)
+    (3072, 32, 8),    # hd 96, GQA 4
+    (768, 8, 8),      # hd 96, MHA
+    (288, 6, 6),      # hd 48, Stories-15M
+    (1536, 32, 8),    # hd 48, GQA 4
+    (1024, 32, 8),    # hd 32, GQA 4
+    (256, 16, 4),     # hd 16, GQA 4
+    (4096, 32, 8),    # hd 128, Llama-3-8B: one tiling
+    (1024, 4, 4),     # hd 256: one tiling
 ]
 
 
-@pytest.mark.parametrize("dim,heads,kv_heads", HD64_SHAPES)
-def test_decode_hd64_tilings_against_oracle(dim, heads, kv_heads):
-    """hd 64 picks its tiling by length.  The policy at every length up to
-    past the wide tiling's start against hd64_plan; then decode with append
-    at the first and last length of each run of one (tiling, split count)
-    change and at a ragged length inside each tiling, against the oracle, with
-    the appended K/V rows bit for bit."""
+@pytest.mark.parametrize("dim,heads,kv_heads", TILING_SHAPES)
+def test_decode_tilings_against_oracle(dim, heads, kv_heads):
+    """The decode tiling and split count picked by length.  The policy at
+    every length up to 300 rows past its last change of tiling against
+    decode_plan;
+    then decode with append at the first and last length of each run of one
+    (tiling, split count) and inside each tiling, against the oracle, with the
+    appended K/V rows bit for bit."""
     torch = pytest.importorskip("torch")
     cus = torch.cuda.get_device_properties(0).multi_processor_count
+    hd = dim // heads
+    last = "wide" if hd in (64, 96) else "base"  # the regime long sequences end in
     runs = []  # [first length, last length, (ns, tile, tiling)]
+    since = 0  # where the tiling last changed
     with P.AttentionContext(dim, heads, kv_heads, 16, 1) as probe:
         n = 1
         while True:
-            want = hd64_plan(n, heads, kv_heads, cus)
+            want = decode_plan(n, heads, kv_heads, hd, cus)
             got = probe.decode_splits(n)
             assert got == want[:2], (n, got, want)
             if runs and runs[-1][2] == want:
                 runs[-1][1] = n
             else:
+                if not runs or runs[-1][2][2] != want[2] or (want[0] > 1) != (runs[-1][2][0] > 1):
+                    since = n
                 runs.append([n, n, want])
-            if want[2] == "wide" and n - runs[-1][0] > 300:
+            if want[2] == last and want[0] > 1 and n - since > 300:
                 break
             n += 1
     tilings = {r[2][2] for r in runs}
-    assert {"base", "wide"} <= tilings, tilings
     picks = set()
-    for first, last, _ in runs:
-        picks |= {first, last}
+    for first, end, _ in runs:
+        picks |= {first, end}
     for t in tilings:
         r = max((r for r in runs if r[2][2] == t), key=lambda r: r[1] - r[0])
         mid = (r[0] + r[1]) // 2
         picks.add(mid if mid % r[2][1] else mid + 1 if mid < r[1] else mid - 1)
-    # the decode positions p = length - 1; runs of one split count change often
-    # at short lengths, so keep the transitions between tilings and a sample
+    # runs of one split count change every tile at short lengths: keep the
+    # transitions between tilings and a sample of the rest
     keys = sorted(picks)
     trans = set()
     for a, b in zip(runs, runs[1:]):
@@ -784,7 +809,7 @@ def test_decode_hd64_tilings_against_oracle(dim, heads, kv_heads):
     cfg = orc.Cfg(dim, heads, kv_heads, msl, 1, 1e4)
     kvd = cfg.kv_dim
     om = orc.OracleModel(cfg)
-    log(f"hd 64 {heads}/{kv_heads}: tilings {[(r[0], r[1], r[2]) for r in runs if r[2][2] != 'base' or r[2][0] == 1][:6]} ...; lengths {sample}")
+    log(f"hd {hd} {heads}/{kv_heads}: tilings {sorted(tilings)}, lengths {sample}")
     with P.AttentionContext(dim, heads, kv_heads, msl, 1) as ctx:
         top = msl - 1
         kr = gen([97, dim], (top, kvd))
@@ -798,7 +823,7 @@ def test_decode_hd64_tilings_against_oracle(dim, heads, kv_heads):
             q1, k1, v1 = gen([99, p], dim), gen([100, p], kvd), gen([101, p], kvd)
             g = ctx.decode(0, p, q1, k1, v1)
             r = om.decode(0, p, q1, k1, v1)
-            assert_close(g, r, what=f"decode at {p} ({hd64_plan(n, heads, kv_heads, cus)})")
+            assert_close(g, r, what=f"decode at {p} ({decode_plan(n, heads, kv_heads, hd, cus)})")
             assert_bitwise(ctx.kv_read(0, 0, p, 1), om.k_cache(0)[p:p + 1], f"K row {p}")
             assert_bitwise(ctx.kv_read(0, 1, p, 1), om.v_cache(0)[p:p + 1], f"V row {p}")
 
