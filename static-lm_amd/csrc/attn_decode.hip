@@ -754,8 +754,29 @@ TilingDims tiling_dims(int head_dim, Tiling t) {
     }
 }
 
-bool tiling_short(int head_dim) { return head_dim <= 96; }  // has_short<HD>()
-bool tiling_wide(int head_dim) { return head_dim == 64 || head_dim == 96; }
+// has_short / has_wide of a runtime head dim
+template <bool (*F16)(), bool (*F32)(), bool (*F48)(), bool (*F64)(), bool (*F96)(),
+          bool (*F128)(), bool (*F256)()>
+bool by_head_dim(int head_dim) {
+    switch (head_dim) {
+        case 16: return F16();
+        case 32: return F32();
+        case 48: return F48();
+        case 64: return F64();
+        case 96: return F96();
+        case 128: return F128();
+        case 256: return F256();
+        default: return false;
+    }
+}
+bool tiling_short(int head_dim) {
+    return by_head_dim<has_short<16>, has_short<32>, has_short<48>, has_short<64>, has_short<96>,
+                       has_short<128>, has_short<256>>(head_dim);
+}
+bool tiling_wide(int head_dim) {
+    return by_head_dim<has_wide<16>, has_wide<32>, has_wide<48>, has_wide<64>, has_wide<96>,
+                       has_wide<128>, has_wide<256>>(head_dim);
+}
 
 int decode_one_split_tiles(const Shape& s) {
     switch (s.head_dim) {
