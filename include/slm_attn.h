@@ -231,8 +231,10 @@ int slm_attn_profile_read(slm_attn_ctx* ctx, slm_kernel_stat* out /* [SLM_K_COUN
 
 /* Split-K layout the decode kernel uses at a given sequence length: positions
  * are cut into tiles of *tile rows and split s of *n_splits reads tiles s,
- * s + n_splits, s + 2*n_splits, ...  A pure function of seq_len, the config and
- * the device's CU count, so results reproduce run to run on a device. */
+ * s + n_splits, s + 2*n_splits, ...  The tile length depends on the length too
+ * for head_dim 16-96 (shorter tiles for short sequences).  A pure function of
+ * seq_len, the config and the device's CU count, so results reproduce run to
+ * run on a device. */
 int slm_attn_decode_splits(const slm_attn_ctx* ctx, int32_t seq_len,
                            int32_t* n_splits, int32_t* tile);
 
