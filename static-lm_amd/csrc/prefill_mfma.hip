@@ -765,9 +765,19 @@ hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
         // against 125.6; 1024 rows (two workgroups per CU) even; 2048 / 3072
         // rows 368 / 785 against 301 / 607 us (158 VGPRs: one 8-wave workgroup
         // per CU against three 4-wave ones); below 256 rows 13% slower.
+        // With one head and four key splits per workgroup (no GQA sharing of
+        // the tiles, 200 VGPRs), while that grid still fits the CUs once: 256
+        // rows 22.2 against 25.6 us (Llama-3-8B shape) and 24.9 against 31.1
+        // (MHA, 32 KV heads, where two heads per workgroup are not possible);
+        // at 512 rows, two rounds of 512 workgroups, 53.2 against 39.7 and
+        // 54.9 against 53.9.
         const long wgs = (long)((pp.n + 16 * t.qs - 1) / (16 * t.qs)) * (s.num_heads / t.hw);
-        if (s.kv_mul % 2 == 0 && pp.n >= 256 && wgs <= s.cus)
-            return launch_t<128, 2, 2, 2, true>(s, pp, st);
+        const long pairs = ((pp.n + 15) / 16 + 1) / 2;
+        if (pp.n >= 256 && wgs <= s.cus) {
+            if (pairs * s.num_heads <= s.cus) return launch_t<128, 1, 2, 4, true>(s, pp, st);
+            if (s.kv_mul % 2 == 0 && pairs * (s.num_heads / 2) <= s.cus)
+                return launch_t<128, 2, 2, 2, true>(s, pp, st);
+        }
     }
     // Short prefills, head_dim <= 64: when the head-group tiling gives fewer
     // than two workgroups per CU, one head and one 16-row query block per

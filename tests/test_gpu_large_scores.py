@@ -314,9 +314,10 @@ def test_decode_large_scores_closed_form(name, p):
 # 128 and hd 96 MHA shapes; the hd 64 (three heads), hd 48 and hd 16 shapes
 # give under two workgroups per CU at these lengths and take the one-head
 # kernel with the key tiles split over four waves; 480 Llama-3-8B-shape rows
-# take the paired-block kernel (two heads, blocks i and n-1-i, two key splits)
+# take the paired-block kernel (two heads, blocks i and n-1-i, two key
+# splits), 256 rows of hd 128 MHA its one-head form (four key splits)
 PREFILL_CASES = [("llama3-8b", 0, 4096), ("llama3-8b", 24, 1000), ("llama3-8b", 100, 480),
-                 ("smollm2", 0, 2048),
+                 ("hd128-mha", 40, 256), ("smollm2", 0, 2048),
                  ("stories15m", 0, 512), ("hd128-mha", 0, 2048), ("hd256-gqa4", 24, 1000),
                  ("hd96-mha", 0, 1024), ("hd32-gqa4", 0, 1024), ("hd16-gqa4", 0, 512)]
 A = (4.0, 4.5, 5.0, 3.5)  # per-head size of q's large component

@@ -193,29 +193,41 @@ def test_llama3_shape_short_prefill_every_row(start, n):
         assert_close(g, ref, what=f"prefill of {n} rows at {start}")
 
 
-def takes_paired_blocks(dim, heads, kv_heads, n, cus=256):
-    """hd 128 prefills of at least 256 rows whose head-group tiling gives at
-    most one workgroup per CU take the paired-block kernel (blocks i and
-    n_qb-1-i, two heads, two key splits) when kv_mul is even."""
+def paired_blocks(dim, heads, kv_heads, n, cus=256):
+    """Which paired-block kernel an hd-128 prefill of n rows takes (blocks i
+    and n_qb-1-i per workgroup), or None: for at least 256 rows whose
+    head-group tiling gives at most one workgroup per CU, one head and four
+    key splits ("h1k4") while pairs x heads fit the CUs, else two heads and
+    two key splits ("h2k2") for an even kv_mul while pairs x heads/2 fit."""
     hd = dim // heads
     kv_mul = heads // kv_heads
     hw, qs = (4, 1) if kv_mul % 4 == 0 else (3, 1) if kv_mul % 3 == 0 else \
         (2, 2) if kv_mul % 2 == 0 else (1, 4)
     wgs = -(-n // (16 * qs)) * (heads // hw)
-    return hd == 128 and kv_mul % 2 == 0 and n >= 256 and wgs <= cus
+    pairs = (-(-n // 16) + 1) // 2
+    if hd != 128 or n < 256 or wgs > cus:
+        return None
+    if pairs * heads <= cus:
+        return "h1k4"
+    if kv_mul % 2 == 0 and pairs * (heads // 2) <= cus:
+        return "h2k2"
+    return None
 
 
-@pytest.mark.parametrize("dim,heads,kv_heads,start,n", [
-    (4096, 32, 8, 0, 256),     # 16 blocks: 8 pairs
-    (4096, 32, 8, 0, 300),     # 19 blocks: the middle pair's second block is its first
-    (4096, 32, 8, 37, 471),    # unaligned start and a partial last block
-    (4096, 32, 8, 1000, 512),  # a long prefix: every block's keys span 48 tiles
-    (2048, 16, 2, 0, 777),     # kv_mul 8: two head pairs per KV head, 49 blocks
-    (1024, 8, 4, 13, 1500),    # kv_mul 2
+@pytest.mark.parametrize("dim,heads,kv_heads,start,n,variant", [
+    (4096, 32, 8, 0, 256, "h1k4"),     # 16 blocks: 8 pairs of one head
+    (4096, 32, 32, 17, 256, "h1k4"),   # MHA (the Llama-2-7B layout), unaligned start
+    (2048, 16, 16, 0, 300, "h1k4"),    # MHA, 19 blocks: the middle pair's second block is its first
+    (1024, 8, 4, 0, 700, "h1k4"),      # kv_mul 2, 44 blocks
+    (4096, 32, 8, 0, 300, "h2k2"),     # 19 blocks, two heads
+    (4096, 32, 8, 37, 471, "h2k2"),    # unaligned start and a partial last block
+    (4096, 32, 8, 1000, 512, "h2k2"),  # a long prefix: every block's keys span 48 tiles
+    (2048, 16, 2, 0, 777, "h2k2"),     # kv_mul 8: two head pairs per KV head, 49 blocks
+    (1024, 8, 4, 13, 1500, "h2k2"),    # kv_mul 2
 ])
-def test_prefill_paired_blocks_every_row(dim, heads, kv_heads, start, n):
+def test_prefill_paired_blocks_every_row(dim, heads, kv_heads, start, n, variant):
     # every row against the oracle, K/V rows bit for bit
-    assert takes_paired_blocks(dim, heads, kv_heads, n)
+    assert paired_blocks(dim, heads, kv_heads, n) == variant
     rows = start + n
     cfg = orc.Cfg(dim, heads, kv_heads, rows, 1, 5e5)
     q = gen([102, start, n], (rows, dim))
