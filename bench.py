@@ -1206,8 +1206,9 @@ def main() -> int:
         extra = {
             "roofline_prefill": {
                 "bound": "mfma",
-                "kernel": "prefill_mfma_kernel<128,4,2,1,32,2,false,true> (causal attention, "
-                          "fp32 v_mfma_f32_16x16x4f32, DMA-fed LDS tiles, 4096 rows)",
+                "kernel": "prefill_mfma_kernel<128,4,2,1,32,2,false,true,1,true> (causal "
+                          "attention, fp32 v_mfma_f32_16x16x4f32, DMA-fed LDS tiles, paired "
+                          "query blocks, 4096 rows)",
                 "achieved": round(pf["kernel_tflops"], 2),
                 "peak": FP32_MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s",

@@ -200,7 +200,7 @@ prefill_mfma_kernel(PrefillParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    static_assert(!PAIR || (QS == 2 && NQT == 1 && !DMA), "pairs: two 16-row blocks");
+    static_assert(!PAIR || (QS == 2 && NQT == 1), "pairs: two 16-row blocks");
     const int hw = PAIR ? (wave / KSP) % HW : wave % HW;
     const int qs = PAIR ? wave / (KSP * HW) : (wave / HW) % QS;
     const int kspl = PAIR ? wave % KSP : wave / NWS;  // key split
@@ -740,21 +740,6 @@ template <int HD>
 hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
     const Tiling t = pick_tiling(s.kv_mul);
     if constexpr (HD == 128) {
-        // Four heads of one KV head and two 16-row query blocks per workgroup
-        // (8 waves), DMA-fed LDS tiles: the same K/V tile serves eight waves,
-        // and two 64 KiB workgroups fit a CU's LDS.  Its grid is half the
-        // other kernel's, so it runs only when that still gives four
-        // workgroups per CU: measured for the Llama-3-8B shape, the DMA kernel
-        // against the register-prefetch one took 73.5 / 48.8 us at 512 rows,
-        // 141 / 114 at 1024, 388 / 324 at 2048, 625 / 619-637 at 3072 and
-        // 985-991 / 1025 at 4096.
-        constexpr int QB = 32;
-        const int n_qb = (pp.n + QB - 1) / QB;
-        if (t.hw == 4 && (long)n_qb * (s.num_heads / 4) >= 4L * s.cus) {
-            hipLaunchKernelGGL((prefill_mfma_kernel<128, 4, 2, 1, 32, 2, false, true>),
-                               dim3(n_qb * (s.num_heads / 4)), dim3(512), 0, st, pp);
-            return hipGetLastError();
-        }
         // Short prefills whose head-group tiling gives at most one workgroup
         // per CU run one wave per SIMD, and the heaviest causal block sets
         // the time (its tiles in series: 16 at 512 rows, against 8.5 on
@@ -777,6 +762,39 @@ hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
             if (pairs * s.num_heads <= s.cus) return launch_t<128, 1, 2, 4, true>(s, pp, st);
             if (s.kv_mul % 2 == 0 && pairs * (s.num_heads / 2) <= s.cus)
                 return launch_t<128, 2, 2, 2, true>(s, pp, st);
+        }
+        // Four heads of one KV head and two 16-row query blocks per workgroup
+        // (8 waves), DMA-fed LDS tiles: the same K/V tile serves eight waves,
+        // and two 64 KiB workgroups fit a CU's LDS.  With consecutive blocks
+        // its grid is half the other kernel's, so that form runs only when it
+        // still gives four workgroups per CU: measured for the Llama-3-8B
+        // shape, the DMA kernel against the register-prefetch one took 73.5 /
+        // 48.8 us at 512 rows, 141 / 114 at 1024, 388 / 324 at 2048, 625 /
+        // 619-637 at 3072 and 985-991 / 1025 at 4096.  With paired blocks (i
+        // and n_qb-1-i, 16 rows each; same bits) every workgroup has the same
+        // work, so the time follows the workgroups per CU: it runs when they
+        // are at most one or a whole number.  Interleaved per call, against
+        // the kernel that ran before: 600 / 768 / 1024 rows (152 / 192 / 256
+        // workgroups) 55.1 / 67.4 / 91 against 62.5 / 80.4 / 115 us, 2048 /
+        // 3072 / 4096 / 5120 / 8192 rows (2, 3, 4, 5, 8 per CU) 270 / 577 /
+        // 997 / 1535 / 3843 against 305 / 607 / 1003 / 1590 / 3880; with
+        // fractions per CU it lost (1152 / 1280 / 2560 / 3584 rows: +16 / +11
+        // / +7 / +7%), and below 512 rows too (64 / 100 / 200 rows +21 / +21
+        // / +9%, 77 rows at start 300 +45%).
+        constexpr int QB = 32;
+        const int n_qb = (pp.n + QB - 1) / QB;
+        if (t.hw == 4) {
+            const long pwgs = (((long)pp.n + 15) / 16 + 1) / 2 * (s.num_heads / 4);
+            if (pp.n >= 512 && (pwgs <= s.cus || pwgs % s.cus == 0)) {
+                hipLaunchKernelGGL((prefill_mfma_kernel<128, 4, 2, 1, 32, 2, false, true, 1, true>),
+                                   dim3(pwgs), dim3(512), 0, st, pp);
+                return hipGetLastError();
+            }
+            if ((long)n_qb * (s.num_heads / 4) >= 4L * s.cus) {
+                hipLaunchKernelGGL((prefill_mfma_kernel<128, 4, 2, 1, 32, 2, false, true>),
+                                   dim3(n_qb * (s.num_heads / 4)), dim3(512), 0, st, pp);
+                return hipGetLastError();
+            }
         }
     }
     // Short prefills, head_dim <= 64: when the head-group tiling gives fewer

@@ -246,6 +246,44 @@ def test_prefill_paired_blocks_every_row(dim, heads, kv_heads, start, n, variant
         assert_close(g, ref, what=f"prefill of {n} rows at {start}")
 
 
+def paired_dma(dim, heads, kv_heads, n, cus=256):
+    """hd-128 prefills of 512 rows or more with kv_mul a multiple of 4 that
+    the short paired kernels leave take the DMA-fed kernel with paired blocks
+    (blocks i and n_qb-1-i, four heads) when its grid is at most the CU count
+    or a whole multiple of it."""
+    kv_mul = heads // kv_heads
+    pwgs = (-(-n // 16) + 1) // 2 * (heads // 4)
+    return (dim // heads == 128 and kv_mul % 4 == 0 and n >= 512
+            and paired_blocks(dim, heads, kv_heads, n, cus) is None
+            and (pwgs <= cus or pwgs % cus == 0))
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads,start,n", [
+    (4096, 32, 8, 5, 2040),    # 128 blocks, 512 workgroups (two per CU), a partial last block
+    (2048, 16, 4, 0, 1520),    # 95 blocks: the middle pair's second block is its first
+    (2048, 16, 2, 19, 1100),   # kv_mul 8: two workgroups' heads share each KV head
+])
+def test_prefill_paired_dma_every_row(dim, heads, kv_heads, start, n):
+    # every row against the oracle, K/V rows bit for bit
+    assert paired_dma(dim, heads, kv_heads, n)
+    rows = start + n
+    cfg = orc.Cfg(dim, heads, kv_heads, rows, 1, 5e5)
+    q = gen([105, start, n], (rows, dim))
+    k = gen([106, start, n], (rows, cfg.kv_dim))
+    v = gen([107, start, n], (rows, cfg.kv_dim))
+    om = orc.OracleModel(cfg)
+    with P.AttentionContext(dim, heads, kv_heads, rows, 1, 5e5) as ctx:
+        log(f"paired-block DMA prefill {heads}/{kv_heads} heads: {n} rows at start {start}")
+        if start:
+            ctx.prefill(0, 0, q[:start], k[:start], v[:start])
+            om.append(0, 0, k[:start], v[:start])
+        g = ctx.prefill(0, start, q[start:], k[start:], v[start:])
+        ref = om.prefill(0, start, q[start:], k[start:], v[start:])
+        assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
+        assert_close(g, ref, what=f"prefill of {n} rows at {start}")
+
+
 def test_long_context_decode_131072():
     w = WORKLOADS["c5"]
     cfg = w.cfg()
