@@ -780,12 +780,15 @@ hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
         // 997 / 1535 / 3843 against 305 / 607 / 1003 / 1590 / 3880; with
         // fractions per CU it lost (1152 / 1280 / 2560 / 3584 rows: +16 / +11
         // / +7 / +7%), and below 512 rows too (64 / 100 / 200 rows +21 / +21
-        // / +9%, 77 rows at start 300 +45%).
+        // / +9%, 77 rows at start 300 +45%).  Pairing halves the grid, so it
+        // runs only where the four-head kernel's grid has more workgroups
+        // than CUs (with one per CU it only idles half of them: hd 96 at 512
+        // rows from start 1000, +32%).
         constexpr int QB = 32;
         const int n_qb = (pp.n + QB - 1) / QB;
         if (t.hw == 4) {
             const long pwgs = (((long)pp.n + 15) / 16 + 1) / 2 * (s.num_heads / 4);
-            if (pp.n >= 512 && (pwgs <= s.cus || pwgs % s.cus == 0)) {
+            if (pp.n >= 512 && wgs > s.cus && (pwgs <= s.cus || pwgs % s.cus == 0)) {
                 hipLaunchKernelGGL((prefill_mfma_kernel<128, 4, 2, 1, 32, 2, false, true, 1, true>),
                                    dim3(pwgs), dim3(512), 0, st, pp);
                 return hipGetLastError();
@@ -810,6 +813,27 @@ hipError_t launch_hd(const Shape& s, const PrefillParams& pp, hipStream_t st) {
         const long wgs = (long)((pp.n + 16 * qs - 1) / (16 * qs)) * (s.num_heads / t.hw);
         const long tiles = ((long)pp.start + pp.n + 31) / 32;  // the heaviest block's
         if (wgs < 2L * s.cus && tiles >= 2L * KSP) return launch_t<HD, 1, 1, KSP>(s, pp, st);
+    }
+    if constexpr (HD <= 96) {
+        // Paired blocks (i and n_qb-1-i) in the four-head register kernel, as
+        // in the DMA-fed one: where the four-head grid has more workgroups
+        // than CUs and the paired grid (8-wave workgroups, one per CU) is at
+        // most one or two per CU.  Interleaved per call against the four-head
+        // kernel, GQA 4 (32 heads): at 1024 rows hd 16 / 32 / 48 / 64 / 96
+        // 23.8 / 35.5 / 48.2 / 53.5 / 77.8 against 26.8 / 38.7 / 54.8 / 63.5 /
+        // 91.9 us, at 2048 rows 55.7 / 87.4 / 123.3 / 149.1 / 222.2 against
+        // 60.8 / 97.2 / 137.9 / 167.6 / 248.9, hd 96 at 768 rows 59.3 against
+        // 66.0; it lost with 1.5 per CU (1536 rows: +1.4 / +2.4% at hd 64 /
+        // 96) and from three per CU (4096 rows: +3.5 / +1.8%, against the
+        // four-head kernel's three 4-wave workgroups per CU); with three heads
+        // per workgroup (SmolLM2 shape) and for MHA it gained nothing or lost
+        // (MHA at 2048 rows +19%).
+        if (t.hw == 4) {
+            const long wgs = (long)((pp.n + 15) / 16) * (s.num_heads / 4);
+            const long pwgs = (((long)pp.n + 15) / 16 + 1) / 2 * (s.num_heads / 4);
+            if (wgs > s.cus && (pwgs <= s.cus || pwgs == 2L * s.cus))
+                return launch_t<HD, 4, 2, 1, true>(s, pp, st);
+        }
     }
     if (t.hw == 4) return launch_t<HD, 4, 1, 1>(s, pp, st);
     if (t.hw == 3) return launch_t<HD, 3, 1, 1>(s, pp, st);

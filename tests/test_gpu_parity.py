@@ -249,13 +249,15 @@ def test_prefill_paired_blocks_every_row(dim, heads, kv_heads, start, n, variant
 def paired_dma(dim, heads, kv_heads, n, cus=256):
     """hd-128 prefills of 512 rows or more with kv_mul a multiple of 4 that
     the short paired kernels leave take the DMA-fed kernel with paired blocks
-    (blocks i and n_qb-1-i, four heads) when its grid is at most the CU count
-    or a whole multiple of it."""
+    (blocks i and n_qb-1-i, four heads) when the four-head grid has more
+    workgroups than CUs and the paired grid is at most the CU count or a
+    whole multiple of it."""
     kv_mul = heads // kv_heads
+    wgs = -(-n // 16) * (heads // 4)
     pwgs = (-(-n // 16) + 1) // 2 * (heads // 4)
     return (dim // heads == 128 and kv_mul % 4 == 0 and n >= 512
             and paired_blocks(dim, heads, kv_heads, n, cus) is None
-            and (pwgs <= cus or pwgs % cus == 0))
+            and wgs > cus and (pwgs <= cus or pwgs % cus == 0))
 
 
 @pytest.mark.parametrize("dim,heads,kv_heads,start,n", [
@@ -274,6 +276,47 @@ def test_prefill_paired_dma_every_row(dim, heads, kv_heads, start, n):
     om = orc.OracleModel(cfg)
     with P.AttentionContext(dim, heads, kv_heads, rows, 1, 5e5) as ctx:
         log(f"paired-block DMA prefill {heads}/{kv_heads} heads: {n} rows at start {start}")
+        if start:
+            ctx.prefill(0, 0, q[:start], k[:start], v[:start])
+            om.append(0, 0, k[:start], v[:start])
+        g = ctx.prefill(0, start, q[start:], k[start:], v[start:])
+        ref = om.prefill(0, start, q[start:], k[start:], v[start:])
+        assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
+        assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
+        assert_close(g, ref, what=f"prefill of {n} rows at {start}")
+
+
+def paired_register(dim, heads, kv_heads, start, n, cus=256):
+    """Prefills of hd 16-96 with kv_mul a multiple of 4 that the one-head
+    key-split kernel leaves take the four-head register kernel with paired
+    blocks when the four-head grid has more workgroups than CUs and the
+    paired grid is at most one or two per CU."""
+    hd, kv_mul = dim // heads, heads // kv_heads
+    wgs = -(-n // 16) * (heads // 4)
+    pwgs = (-(-n // 16) + 1) // 2 * (heads // 4)
+    key_splits = hd <= 64 and wgs < 2 * cus and (start + n + 31) // 32 >= 8
+    return (hd <= 96 and kv_mul % 4 == 0 and not key_splits and wgs > cus
+            and (pwgs <= cus or pwgs == 2 * cus))
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads,start,n", [
+    (3072, 32, 8, 0, 1000),   # hd 96: 63 blocks, the middle pair's second block is its first
+    (3072, 32, 8, 9, 2040),   # hd 96: 128 blocks, two workgroups per CU, partial last block
+    (2048, 32, 8, 0, 2048),   # hd 64 (the Llama-3.2-1B layout)
+    (1024, 32, 8, 3, 1015),   # hd 32: 64 blocks, the last partial
+    (512, 32, 8, 0, 2048),    # hd 16
+])
+def test_prefill_paired_register_every_row(dim, heads, kv_heads, start, n):
+    # every row against the oracle, K/V rows bit for bit
+    assert paired_register(dim, heads, kv_heads, start, n)
+    rows = start + n
+    cfg = orc.Cfg(dim, heads, kv_heads, rows, 1, 5e5)
+    q = gen([108, start, n], (rows, dim))
+    k = gen([109, start, n], (rows, cfg.kv_dim))
+    v = gen([110, start, n], (rows, cfg.kv_dim))
+    om = orc.OracleModel(cfg)
+    with P.AttentionContext(dim, heads, kv_heads, rows, 1, 5e5) as ctx:
+        log(f"paired-block register prefill hd {dim // heads}: {n} rows at start {start}")
         if start:
             ctx.prefill(0, 0, q[:start], k[:start], v[:start])
             om.append(0, 0, k[:start], v[:start])
