@@ -238,6 +238,30 @@ int slm_attn_profile_read(slm_attn_ctx* ctx, slm_kernel_stat* out /* [SLM_K_COUN
 int slm_attn_decode_splits(const slm_attn_ctx* ctx, int32_t seq_len,
                            int32_t* n_splits, int32_t* tile);
 
+/* The kernel a causal prefill of n rows from row start runs (slm_attn_prefill,
+ * slm_attn_prefill_dev and the blocks built on them).  Like the decode split
+ * layout, a pure function of start, n, the config and the device's CU count;
+ * no counterpart in the reference, which has one scalar path: it is for tests
+ * and benchmarks that need to know which kernel ran.  Heads per workgroup are
+ * query heads of one KV head; query blocks are 16 rows; "paired" workgroups
+ * take blocks i and n_blocks-1-i, so every workgroup has the same causal
+ * work.  SLM_ERR_BATCH as slm_attn_prefill for an empty or out-of-range
+ * batch. */
+enum {
+    SLM_PF_FOUR_HEADS = 0,        /* four heads, one block (kv_mul % 4 == 0) */
+    SLM_PF_THREE_HEADS = 1,       /* three heads, one block (kv_mul % 3 == 0) */
+    SLM_PF_TWO_HEADS = 2,         /* two heads, two blocks (kv_mul even) */
+    SLM_PF_ONE_HEAD = 3,          /* one head, four blocks */
+    SLM_PF_KEY_SPLIT = 4,         /* one head, one block, key tiles over four waves (hd <= 64) */
+    SLM_PF_PAIRED_FOUR_HEADS = 5, /* four heads, paired blocks (hd <= 96) */
+    SLM_PF_DMA = 6,               /* hd 128: four heads, two blocks, tiles staged by DMA */
+    SLM_PF_DMA_PAIRED = 7,        /* hd 128: the same with paired blocks */
+    SLM_PF_PAIRED_TWO_HEADS = 8,  /* hd 128: two heads, paired blocks, two key splits */
+    SLM_PF_PAIRED_ONE_HEAD = 9    /* hd 128: one head, paired blocks, four key splits */
+};
+int slm_attn_prefill_kernel(const slm_attn_ctx* ctx, int32_t start, int32_t n,
+                            int32_t* kernel);
+
 /* Library version string. */
 const char* slm_attn_version(void);
 

@@ -66,6 +66,10 @@ GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8
 
 KERNEL_KINDS = ("append", "decode", "combine", "prefill", "rope", "quant", "gemm", "norm",
                 "elem")
+# prefill kernels, numbered as SLM_PF_* (slm_attn_prefill_kernel)
+PREFILL_KERNELS = ("four_heads", "three_heads", "two_heads", "one_head", "key_split",
+                   "paired_four_heads", "dma", "dma_paired", "paired_two_heads",
+                   "paired_one_head")
 
 
 class SlmAttnError(RuntimeError):
@@ -146,6 +150,7 @@ SIGNATURES = {
     "slm_attn_profile": (ctypes.c_int, [_P, _I]),
     "slm_attn_profile_read": (ctypes.c_int, [_P, ctypes.POINTER(_KernelStat)]),
     "slm_attn_decode_splits": (ctypes.c_int, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "slm_attn_prefill_kernel": (ctypes.c_int, [_P, _I, _I, ctypes.POINTER(_I)]),
     "slm_attn_version": (ctypes.c_char_p, []),
     # slm_quant.h
     "slm_q4_matrix_create": (ctypes.c_int, [_I, ctypes.c_void_p, _I, _I, ctypes.POINTER(_P)]),
@@ -525,6 +530,13 @@ class AttentionContext:
         self._check(self.lib.slm_attn_decode_splits(self._h, seq_len, ctypes.byref(ns),
                                                     ctypes.byref(tile)))
         return ns.value, tile.value
+
+    def prefill_kernel(self, start: int, n: int) -> str:
+        """Name (PREFILL_KERNELS) of the kernel a prefill of n rows from row
+        start runs."""
+        k = _I()
+        self._check(self.lib.slm_attn_prefill_kernel(self._h, start, n, ctypes.byref(k)))
+        return PREFILL_KERNELS[k.value]
 
 
 class AttentionGraph:

@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "prefill_plan.h"
 #include "slm_host.h"
 #include "tile_range.h"
 
@@ -940,6 +941,17 @@ int slm_attn_decode_splits(const slm_attn_ctx* c, int32_t seq_len,
     slm::decode_split_policy(c->shape, seq_len, &ns, &t);
     *n_splits = ns;
     *tile = t;
+    return SLM_OK;
+}
+
+int slm_attn_prefill_kernel(const slm_attn_ctx* c, int32_t start, int32_t n,
+                            int32_t* kernel) {
+    if (!c || !kernel) return fail(nullptr, SLM_ERR_ARG, "bad argument");
+    if (n <= 0 || start < 0 || (long)start + n > c->cfg.max_seq_len)
+        return fail(nullptr, SLM_ERR_BATCH,
+                    "batch must be non-empty and start + n <= max_seq_len");
+    const slm::Shape& s = c->shape;
+    *kernel = (int32_t)slm::prefill_plan(s.head_dim, s.num_heads, s.kv_mul, s.cus, start, n);
     return SLM_OK;
 }
 

@@ -183,3 +183,103 @@ def xorshift_f32(n: int, seed: int, lo: float, span: float) -> np.ndarray:
         unit = np.float32(np.float32(s) / umax)
         out[i] = np.float32(np.float32(unit * np.float32(span)) + np.float32(lo))
     return out
+
+
+# Which prefill kernel a batch takes, restated from the dispatch rules for
+# choosing test cases (the library answers the same question through
+# slm_attn_prefill_kernel; tests/test_abi.py checks the two agree).
+def takes_key_splits(dim, heads, kv_heads, start, n, cus=256):
+    """Whether a prefill takes the one-head key-split kernel (prefill_plan.h):
+    head_dim <= 64, fewer than two workgroups per CU in the
+    head-group tiling, at least 8 key tiles in the heaviest block."""
+    hd = dim // heads
+    kv_mul = heads // kv_heads
+    hw = 4 if kv_mul % 4 == 0 else 3 if kv_mul % 3 == 0 else 2 if kv_mul % 2 == 0 else 1
+    qs = {4: 1, 3: 1, 2: 2, 1: 4}[hw]
+    wgs = -(-n // (16 * qs)) * (heads // hw)
+    return hd <= 64 and wgs < 2 * cus and (start + n + 31) // 32 >= 8
+
+
+def paired_blocks(dim, heads, kv_heads, n, cus=256):
+    """Which paired-block kernel an hd-128 prefill of n rows takes (blocks i
+    and n_qb-1-i per workgroup), or None: for at least 256 rows whose
+    head-group tiling gives at most one workgroup per CU, one head and four
+    key splits ("h1k4") while pairs x heads fit the CUs, else two heads and
+    two key splits ("h2k2") for an even kv_mul while pairs x heads/2 fit."""
+    hd = dim // heads
+    kv_mul = heads // kv_heads
+    hw, qs = (4, 1) if kv_mul % 4 == 0 else (3, 1) if kv_mul % 3 == 0 else \
+        (2, 2) if kv_mul % 2 == 0 else (1, 4)
+    wgs = -(-n // (16 * qs)) * (heads // hw)
+    pairs = (-(-n // 16) + 1) // 2
+    if hd != 128 or n < 256 or wgs > cus:
+        return None
+    if pairs * heads <= cus:
+        return "h1k4"
+    if kv_mul % 2 == 0 and pairs * (heads // 2) <= cus:
+        return "h2k2"
+    return None
+
+
+def paired_dma(dim, heads, kv_heads, n, cus=256):
+    """hd-128 prefills of 512 rows or more with kv_mul a multiple of 4 that
+    the short paired kernels leave take the DMA-fed kernel with paired blocks
+    (blocks i and n_qb-1-i, four heads) when the four-head grid has more
+    workgroups than CUs and the paired grid is at most the CU count or a
+    whole multiple of it."""
+    kv_mul = heads // kv_heads
+    wgs = -(-n // 16) * (heads // 4)
+    pwgs = (-(-n // 16) + 1) // 2 * (heads // 4)
+    return (dim // heads == 128 and kv_mul % 4 == 0 and n >= 512
+            and paired_blocks(dim, heads, kv_heads, n, cus) is None
+            and wgs > cus and (pwgs <= cus or pwgs % cus == 0))
+
+
+def paired_register(dim, heads, kv_heads, start, n, cus=256):
+    """Prefills of hd 16-96 with kv_mul a multiple of 4 that the one-head
+    key-split kernel leaves take the four-head register kernel with paired
+    blocks when the four-head grid has more workgroups than CUs and the
+    paired grid is at most one or two per CU."""
+    hd, kv_mul = dim // heads, heads // kv_heads
+    wgs = -(-n // 16) * (heads // 4)
+    pwgs = (-(-n // 16) + 1) // 2 * (heads // 4)
+    key_splits = hd <= 64 and wgs < 2 * cus and (start + n + 31) // 32 >= 8
+    return (hd <= 96 and kv_mul % 4 == 0 and not key_splits and wgs > cus
+            and (pwgs <= cus or pwgs == 2 * cus))
+
+
+# Prefill kernels (slm_attn_prefill_kernel, static-lm_amd PREFILL_KERNELS) and
+# a batch that takes each one on a 256-CU device.
+SWEEP_TARGETED = [
+    # dim, heads, kv_heads, start, n, kernel
+    (2048, 32, 8, 0, 100, "four_heads"),          # hd 64 GQA 4, 56 workgroups
+    (576, 9, 3, 0, 64, "three_heads"),            # the SmolLM2-135M shape, two key tiles
+    (1536, 16, 8, 5, 200, "two_heads"),           # hd 96, kv_mul 2
+    (768, 16, 16, 0, 40, "one_head"),             # hd 48 MHA
+    (576, 9, 3, 0, 512, "key_split"),             # the SmolLM2-135M shape, 512 rows
+    (3072, 32, 8, 0, 1024, "paired_four_heads"),  # hd 96 GQA 4, 256 paired workgroups
+    (8192, 64, 16, 3, 2100, "dma"),               # hd 128, 1056 workgroups (not a multiple of 256)
+    (4096, 32, 8, 0, 1024, "dma_paired"),         # the Llama-3-8B shape, 256 paired workgroups
+    (4096, 32, 8, 0, 300, "paired_two_heads"),    # the Llama-3-8B shape, 10 pairs
+    (4096, 32, 8, 0, 256, "paired_one_head"),     # the Llama-3-8B shape, 8 pairs
+]
+
+
+def sweep_random_cases(count=30, seed=20261202):
+    """Seeded random shapes and batches: (dim, heads, kv_heads, start, n).
+    Head dims the library compiles, kv_mul 1/2/3/4/8 with 1-8 KV heads (at
+    most 64 query heads), configs the reference accepts (dim and kv_dim
+    multiples of 32), starts 0-1499 half the time, n log-uniform in 1-2600."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        hd = int(rng.choice((16, 32, 48, 64, 96, 128, 256)))
+        kv_mul = int(rng.choice((1, 2, 3, 4, 8)))
+        kvh = int(rng.choice((1, 2, 3, 4, 8)))
+        heads = kvh * kv_mul
+        if heads > 64 or (heads * hd) % 32 or (kvh * hd) % 32:
+            continue
+        start = int(rng.integers(0, 1500)) if rng.random() < 0.5 else 0
+        n = max(1, int(np.exp(rng.uniform(0.0, np.log(2600.0)))))
+        out.append((heads * hd, heads, kvh, start, n))
+    return out

@@ -6,7 +6,8 @@ import subprocess
 
 import pytest
 
-from slm_testlib import load_product
+from slm_testlib import (SWEEP_TARGETED, load_product, paired_blocks, paired_dma,
+                         paired_register, sweep_random_cases, takes_key_splits)
 
 P = load_product()
 
@@ -147,6 +148,111 @@ def test_prefill_tile_range_is_bounded_by_the_tile(tmp_path):
     # what the old 32-bit product gave for the first case: the wrap the
     # clamp removes
     assert (1048600 * 1024 * 4) % (1 << 32) == 24 * row
+
+
+PLAN_PROBE = r"""
+#include <stdio.h>
+#include "prefill_plan.h"
+int main(void) {
+    int hd, heads, kv_mul, cus, start, n;
+    while (scanf("%d %d %d %d %d %d", &hd, &heads, &kv_mul, &cus, &start, &n) == 6)
+        printf("%d\n", (int)slm::prefill_plan(hd, heads, kv_mul, cus, start, n));
+    return 0;
+}
+"""
+
+
+@pytest.fixture(scope="module")
+def prefill_plan(tmp_path_factory):
+    """csrc/prefill_plan.h compiled for the host: kernel names for a list of
+    (head_dim, heads, kv_mul, cus, start, n)."""
+    d = tmp_path_factory.mktemp("plan")
+    src = d / "plan.cpp"
+    src.write_text(PLAN_PROBE)
+    exe = d / "plan"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror",
+                    f"-I{P.PKG_DIR / 'csrc'}", str(src), "-o", str(exe)], check=True)
+
+    def plan(cases):
+        inp = "".join(" ".join(str(x) for x in c) + "\n" for c in cases)
+        out = subprocess.run([str(exe)], input=inp, capture_output=True, text=True,
+                             check=True).stdout.split()
+        assert len(out) == len(cases)
+        return [P.PREFILL_KERNELS[int(x)] for x in out]
+    return plan
+
+
+def _plan_grid():
+    ns = sorted(set(range(1, 41)) | set(range(41, 9000, 37)) |
+                {m + d for m in (256, 512, 1024, 2048, 4096, 8192) for d in (-17, -1, 0, 1, 15)})
+    for hd in (16, 32, 48, 64, 96, 128, 256):
+        for kv_mul in (1, 2, 3, 4, 8):
+            for kvh in (1, 2, 4, 8):
+                for cus in (256, 32):
+                    for start in (0, 7, 1000):
+                        for n in ns:
+                            yield hd, kvh * kv_mul, kv_mul, cus, start, n
+
+
+def test_prefill_plan_picks_only_compiled_kernels(prefill_plan):
+    # the launcher has each kernel for some head dims and head groupings only
+    # (anything else returns hipErrorInvalidValue); the plan must never pick
+    # one outside them
+    def compiled(hd, kv_mul, k):
+        return {"four_heads": kv_mul % 4 == 0, "three_heads": kv_mul % 3 == 0,
+                "two_heads": kv_mul % 2 == 0, "one_head": True, "key_split": hd <= 64,
+                "paired_four_heads": hd <= 96 and kv_mul % 4 == 0,
+                "dma": hd == 128 and kv_mul % 4 == 0, "dma_paired": hd == 128 and kv_mul % 4 == 0,
+                "paired_two_heads": hd == 128 and kv_mul % 2 == 0,
+                "paired_one_head": hd == 128}[k]
+    grid = list(_plan_grid())
+    got = prefill_plan(grid)
+    bad = [(c, k) for c, k in zip(grid, got) if not compiled(c[0], c[2], k)]
+    assert not bad, bad[:5]
+    assert set(got) == set(P.PREFILL_KERNELS)
+
+
+def test_prefill_plan_agrees_with_the_restated_rules(prefill_plan):
+    # two codings of the same dispatch rules: the header the library compiles
+    # and the test library's restatement used to choose parity cases
+    grid = list(_plan_grid())
+    got = prefill_plan(grid)
+    for (hd, heads, kv_mul, cus, start, n), k in zip(grid, got):
+        dim, kvh = heads * hd, heads // kv_mul
+        case = (hd, heads, kv_mul, cus, start, n, k)
+        assert (k == "key_split") == takes_key_splits(dim, heads, kvh, start, n, cus), case
+        pb = paired_blocks(dim, heads, kvh, n, cus)
+        assert (k == "paired_one_head") == (pb == "h1k4"), case
+        assert (k == "paired_two_heads") == (pb == "h2k2"), case
+        assert (k == "dma_paired") == paired_dma(dim, heads, kvh, n, cus), case
+        assert (k == "paired_four_heads") == paired_register(dim, heads, kvh, start, n, cus), case
+
+
+def test_dispatch_sweep_reaches_every_prefill_kernel(prefill_plan):
+    # the GPU sweep's targeted batches take the kernels they name on a 256-CU
+    # device, and together reach every prefill kernel
+    cases = [(dim // heads, heads, heads // kvh, 256, start, n)
+             for dim, heads, kvh, start, n, _ in SWEEP_TARGETED]
+    got = prefill_plan(cases)
+    assert got == [c[5] for c in SWEEP_TARGETED]
+    assert set(got) == set(P.PREFILL_KERNELS)
+    rnd = sweep_random_cases()
+    kinds = prefill_plan([(dim // heads, heads, heads // kvh, 256, start, n)
+                          for dim, heads, kvh, start, n in rnd])
+    assert len(set(kinds)) >= 5, kinds
+
+
+def test_prefill_kernel_query_checks_its_arguments():
+    lib = P.load_library()
+    k = ctypes.c_int32(-1)
+    assert lib.slm_attn_prefill_kernel(None, 0, 1, ctypes.byref(k)) == P.ERR_ARG
+    assert k.value == -1
+
+
+def test_header_numbers_the_prefill_kernels_like_the_binding():
+    text = P.HEADER_PATH.read_text()
+    for i, name in enumerate(P.PREFILL_KERNELS):
+        assert f"SLM_PF_{name.upper()} = {i}," in text or f"SLM_PF_{name.upper()} = {i} " in text, name
 
 
 def test_header_declares_error_codes_the_binding_uses():

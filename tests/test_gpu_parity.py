@@ -17,7 +17,8 @@ import pytest
 
 from oracle import py_oracle as orc
 from slm_testlib import (WORKLOADS, Workload, assert_bitwise, assert_close, gen, layer_inputs,
-                         load_product, prefilled_rows)
+                         load_product, paired_blocks, paired_dma, paired_register,
+                         prefilled_rows, takes_key_splits)
 
 P = load_product()
 pytestmark = pytest.mark.gpu
@@ -193,27 +194,6 @@ def test_llama3_shape_short_prefill_every_row(start, n):
         assert_close(g, ref, what=f"prefill of {n} rows at {start}")
 
 
-def paired_blocks(dim, heads, kv_heads, n, cus=256):
-    """Which paired-block kernel an hd-128 prefill of n rows takes (blocks i
-    and n_qb-1-i per workgroup), or None: for at least 256 rows whose
-    head-group tiling gives at most one workgroup per CU, one head and four
-    key splits ("h1k4") while pairs x heads fit the CUs, else two heads and
-    two key splits ("h2k2") for an even kv_mul while pairs x heads/2 fit."""
-    hd = dim // heads
-    kv_mul = heads // kv_heads
-    hw, qs = (4, 1) if kv_mul % 4 == 0 else (3, 1) if kv_mul % 3 == 0 else \
-        (2, 2) if kv_mul % 2 == 0 else (1, 4)
-    wgs = -(-n // (16 * qs)) * (heads // hw)
-    pairs = (-(-n // 16) + 1) // 2
-    if hd != 128 or n < 256 or wgs > cus:
-        return None
-    if pairs * heads <= cus:
-        return "h1k4"
-    if kv_mul % 2 == 0 and pairs * (heads // 2) <= cus:
-        return "h2k2"
-    return None
-
-
 @pytest.mark.parametrize("dim,heads,kv_heads,start,n,variant", [
     (4096, 32, 8, 0, 256, "h1k4"),     # 16 blocks: 8 pairs of one head
     (4096, 32, 32, 17, 256, "h1k4"),   # MHA (the Llama-2-7B layout), unaligned start
@@ -236,6 +216,8 @@ def test_prefill_paired_blocks_every_row(dim, heads, kv_heads, start, n, variant
     om = orc.OracleModel(cfg)
     with P.AttentionContext(dim, heads, kv_heads, rows, 1, 5e5) as ctx:
         log(f"paired-block prefill {heads}/{kv_heads} heads: {n} rows at start {start}")
+        assert ctx.prefill_kernel(start, n) == {"h1k4": "paired_one_head",
+                                                "h2k2": "paired_two_heads"}[variant]
         if start:
             ctx.prefill(0, 0, q[:start], k[:start], v[:start])
             om.append(0, 0, k[:start], v[:start])
@@ -244,20 +226,6 @@ def test_prefill_paired_blocks_every_row(dim, heads, kv_heads, start, n, variant
         assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
         assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
         assert_close(g, ref, what=f"prefill of {n} rows at {start}")
-
-
-def paired_dma(dim, heads, kv_heads, n, cus=256):
-    """hd-128 prefills of 512 rows or more with kv_mul a multiple of 4 that
-    the short paired kernels leave take the DMA-fed kernel with paired blocks
-    (blocks i and n_qb-1-i, four heads) when the four-head grid has more
-    workgroups than CUs and the paired grid is at most the CU count or a
-    whole multiple of it."""
-    kv_mul = heads // kv_heads
-    wgs = -(-n // 16) * (heads // 4)
-    pwgs = (-(-n // 16) + 1) // 2 * (heads // 4)
-    return (dim // heads == 128 and kv_mul % 4 == 0 and n >= 512
-            and paired_blocks(dim, heads, kv_heads, n, cus) is None
-            and wgs > cus and (pwgs <= cus or pwgs % cus == 0))
 
 
 @pytest.mark.parametrize("dim,heads,kv_heads,start,n", [
@@ -276,6 +244,7 @@ def test_prefill_paired_dma_every_row(dim, heads, kv_heads, start, n):
     om = orc.OracleModel(cfg)
     with P.AttentionContext(dim, heads, kv_heads, rows, 1, 5e5) as ctx:
         log(f"paired-block DMA prefill {heads}/{kv_heads} heads: {n} rows at start {start}")
+        assert ctx.prefill_kernel(start, n) == "dma_paired"
         if start:
             ctx.prefill(0, 0, q[:start], k[:start], v[:start])
             om.append(0, 0, k[:start], v[:start])
@@ -284,19 +253,6 @@ def test_prefill_paired_dma_every_row(dim, heads, kv_heads, start, n):
         assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
         assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
         assert_close(g, ref, what=f"prefill of {n} rows at {start}")
-
-
-def paired_register(dim, heads, kv_heads, start, n, cus=256):
-    """Prefills of hd 16-96 with kv_mul a multiple of 4 that the one-head
-    key-split kernel leaves take the four-head register kernel with paired
-    blocks when the four-head grid has more workgroups than CUs and the
-    paired grid is at most one or two per CU."""
-    hd, kv_mul = dim // heads, heads // kv_heads
-    wgs = -(-n // 16) * (heads // 4)
-    pwgs = (-(-n // 16) + 1) // 2 * (heads // 4)
-    key_splits = hd <= 64 and wgs < 2 * cus and (start + n + 31) // 32 >= 8
-    return (hd <= 96 and kv_mul % 4 == 0 and not key_splits and wgs > cus
-            and (pwgs <= cus or pwgs == 2 * cus))
 
 
 @pytest.mark.parametrize("dim,heads,kv_heads,start,n", [
@@ -317,6 +273,7 @@ def test_prefill_paired_register_every_row(dim, heads, kv_heads, start, n):
     om = orc.OracleModel(cfg)
     with P.AttentionContext(dim, heads, kv_heads, rows, 1, 5e5) as ctx:
         log(f"paired-block register prefill hd {dim // heads}: {n} rows at start {start}")
+        assert ctx.prefill_kernel(start, n) == "paired_four_heads"
         if start:
             ctx.prefill(0, 0, q[:start], k[:start], v[:start])
             om.append(0, 0, k[:start], v[:start])
@@ -621,18 +578,6 @@ def test_prefill_shapes_and_ragged_batches(dim, heads, kv_heads, start, n):
                              what=f"row {b} at {start + b}")
 
 
-def takes_key_splits(dim, heads, kv_heads, start, n, cus=256):
-    """Whether a prefill takes the one-head key-split kernel (prefill_mfma.hip,
-    launch_hd): head_dim <= 64, fewer than two workgroups per CU in the
-    head-group tiling, at least 8 key tiles in the heaviest block."""
-    hd = dim // heads
-    kv_mul = heads // kv_heads
-    hw = 4 if kv_mul % 4 == 0 else 3 if kv_mul % 3 == 0 else 2 if kv_mul % 2 == 0 else 1
-    qs = {4: 1, 3: 1, 2: 2, 1: 4}[hw]
-    wgs = -(-n // (16 * qs)) * (heads // hw)
-    return hd <= 64 and wgs < 2 * cus and (start + n + 31) // 32 >= 8
-
-
 @pytest.mark.parametrize("dim,heads,kv_heads", [
     (576, 9, 3),     # hd 64, kv_mul 3 (SmolLM2-135M)
     (1024, 16, 16),  # hd 64, MHA
@@ -655,6 +600,7 @@ def test_prefill_key_splits_every_row(dim, heads, kv_heads, start, n):
     v = gen([83, dim, n], (rows, cfg.kv_dim))
     om = orc.OracleModel(cfg)
     with P.AttentionContext(dim, heads, kv_heads, rows, 1) as ctx:
+        assert ctx.prefill_kernel(start, n) == "key_split"
         if start:
             ctx.prefill(0, 0, q[:start], k[:start], v[:start])
             om.prefill(0, 0, q[:start], k[:start], v[:start])
