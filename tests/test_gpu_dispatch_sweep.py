@@ -84,3 +84,14 @@ def test_dispatch_sweep_against_oracle(dim, heads, kv_heads, start, n, kernel):
             assert_close(got, ref, what=f"decode at {p}")
         assert_bitwise(ctx.kv_read(0, 0, 0, rows), om.k_cache(0)[:rows], "K rows")
         assert_bitwise(ctx.kv_read(0, 1, 0, rows), om.v_cache(0)[:rows], "V rows")
+
+
+def test_prefill_kernel_query_rejects_batches_the_prefill_rejects():
+    # the same checks and codes as slm_attn_prefill (SLM_ERR_BATCH); a batch
+    # ending at max_seq_len is accepted
+    with P.AttentionContext(4096, 32, 8, 300, 1, 5e5) as ctx:
+        assert ctx.prefill_kernel(0, 300) == "paired_two_heads"
+        for start, n in ((0, 0), (-1, 4), (290, 11), (300, 1)):
+            with pytest.raises(P.SlmAttnError) as e:
+                ctx.prefill_kernel(start, n)
+            assert e.value.code == P.ERR_BATCH, (start, n)
