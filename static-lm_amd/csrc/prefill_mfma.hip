@@ -27,6 +27,10 @@
 // Online softmax runs in the log2 domain (q pre-scaled by log2(e)/sqrt(hd));
 // the running max is reduced across the four lane groups each tile, the
 // running sum stays a per-lane partial until the end.
+//
+// Which form of the kernel a batch runs (heads and blocks per workgroup,
+// paired blocks, key splits, DMA-fed tiles) is decided in prefill_plan.h,
+// with the measurements behind each rule.
 #include <math.h>
 
 #include <type_traits>
